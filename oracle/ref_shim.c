@@ -1,0 +1,176 @@
+/*
+ * ref_shim.c -- harness linked with the reference's own hot-path sources
+ * (compiled in place from the reference tree by oracle/ref.mk) into
+ * oracle/_ref/libvspec_ref.so.
+ *
+ * TEST INFRASTRUCTURE ONLY.  It gives Python (ctypes) opaque handles to the
+ * reference's structs and restates the two reference call sites that do not
+ * compile standalone:
+ *   - the paged gather loop of vspec_py_kv_cache_read (capi.c:2263-2299), which
+ *     lives in a 2.8k-line file with many dependencies;
+ *   - the GQA head mapping of the Python runtime (runtime_inference.py:151,1419:
+ *     kv_h = h // group), which calls the MHA-only attention_ref per head.
+ * Everything numeric is done by the reference's functions.
+ */
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include "vspec/attention/attention.h"
+#include "vspec/attention/kv_cache.h"
+#include "vspec/attention/kv_paged_cache.h"
+#include "vspec/kernel/backend.h"
+#include "vspec/kernel/context.h"
+
+/* ---- paged cache handles ---- */
+VspecKVPagedCache* vr_paged_new(size_t page_tokens, size_t max_pages, size_t num_heads,
+                                size_t head_dim) {
+    VspecKVPagedCache* c = (VspecKVPagedCache*)calloc(1, sizeof(VspecKVPagedCache));
+    const size_t n = page_tokens * max_pages * num_heads * head_dim;
+    float* k = (float*)calloc(n ? n : 1, sizeof(float));
+    float* v = (float*)calloc(n ? n : 1, sizeof(float));
+    if (!c || !k || !v || !vspec_kv_paged_cache_init(c, k, v, page_tokens, max_pages, num_heads, head_dim)) {
+        free(c);
+        free(k);
+        free(v);
+        return NULL;
+    }
+    return c;
+}
+
+void vr_paged_free(VspecKVPagedCache* c) {
+    if (!c) return;
+    free(c->key_pages);
+    free(c->value_pages);
+    free(c);
+}
+
+const float* vr_paged_key_pages(const VspecKVPagedCache* c) { return c->key_pages; }
+const float* vr_paged_value_pages(const VspecKVPagedCache* c) { return c->value_pages; }
+
+/* Session page list (uint16 page ids as stored by the reference). */
+size_t vr_paged_session_pages(const VspecKVPagedCache* c, uint64_t session_id, uint32_t* out,
+                              size_t cap) {
+    for (size_t i = 0; i < VSPEC_KV_PAGED_MAX_SESSIONS; ++i) {
+        if (c->sessions[i].active && c->sessions[i].session_id == session_id) {
+            size_t n = c->sessions[i].page_count;
+            for (size_t j = 0; j < n && j < cap; ++j) out[j] = c->sessions[i].pages[j];
+            return n;
+        }
+    }
+    return 0;
+}
+
+/* Per-page metadata: used tokens and ref count. */
+void vr_paged_page_meta(const VspecKVPagedCache* c, size_t page, uint32_t* allocated,
+                        uint32_t* used, uint32_t* refc) {
+    *allocated = c->page_meta[page].allocated;
+    *used = c->page_meta[page].used_tokens;
+    *refc = c->page_meta[page].ref_count;
+}
+
+void vr_paged_stats(const VspecKVPagedCache* c, uint64_t* out6) {
+    VspecKVPagedStats s;
+    vspec_kv_paged_stats(c, &s);
+    out6[0] = s.page_alloc_count;
+    out6[1] = s.page_reuse_count;
+    out6[2] = s.evict_session_count;
+    out6[3] = s.append_token_count;
+    out6[4] = s.free_pages;
+    out6[5] = s.active_sessions;
+}
+
+/* capi.c:2263-2299 gather loop over vspec_kv_paged_get_token_ptr. */
+size_t vr_paged_read(const VspecKVPagedCache* c, uint64_t session_id, float* out_keys,
+                     float* out_values, size_t max_tokens) {
+    const size_t stride = c->num_heads * c->head_dim;
+    size_t total = vspec_kv_paged_session_tokens(c, session_id);
+    if (max_tokens > 0u && total > max_tokens) total = max_tokens;
+    for (size_t t = 0; t < total; ++t) {
+        for (size_t h = 0; h < c->num_heads; ++h) {
+            const float* kp = NULL;
+            const float* vp = NULL;
+            if (!vspec_kv_paged_get_token_ptr(c, session_id, t, h, &kp, &vp)) return t;
+            for (size_t d = 0; d < c->head_dim; ++d) {
+                const size_t base = t * stride + h * c->head_dim + d;
+                out_keys[base] = kp[d];
+                out_values[base] = vp[d];
+            }
+        }
+    }
+    return total;
+}
+
+/* ---- contiguous cache + attention through the CPU backend ---- */
+
+/* attention_ref over a contiguous [T][H][D] fp32 cache via the registered CPU
+ * backend (cpu_backend.c:40-51 -> attention_ref.c:7-88). */
+void vr_attention_mha(const float* q, const float* key, const float* value, size_t tokens,
+                      size_t heads, size_t head_dim, float* out) {
+    VspecKVCache cache;
+    if (!vspec_kv_cache_init(&cache, (float*)key, (float*)value, tokens ? tokens : 1, heads, head_dim)) {
+        return;
+    }
+    cache.current_tokens = tokens;
+    VspecBackend be = vspec_make_cpu_backend();
+    VspecKernelContext ctx;
+    memset(&ctx, 0, sizeof(ctx));
+    ctx.input = (void*)q;
+    ctx.weight = &cache;
+    ctx.output = out;
+    be.launch_attention(&ctx);
+}
+
+/* GQA decode for one sequence: q/out [Hq][D], key/value [T][Hkv][D].
+ * The runtime maps query head h to kv head h / G.  For each group slot g the
+ * sub-query collects heads h = kv_h*G + g (kv_h = 0..Hkv-1), which the MHA
+ * attention_ref then pairs with kv head kv_h. */
+void vr_attention_gqa(const float* q, const float* key, const float* value, size_t tokens,
+                      size_t hq, size_t hkv, size_t head_dim, float* out) {
+    const size_t group = hq / hkv;
+    float* qs = (float*)malloc(hkv * head_dim * sizeof(float));
+    float* os = (float*)malloc(hkv * head_dim * sizeof(float));
+    if (!qs || !os) { free(qs); free(os); return; }
+    for (size_t g = 0; g < group; ++g) {
+        for (size_t k = 0; k < hkv; ++k) {
+            memcpy(qs + k * head_dim, q + (k * group + g) * head_dim, head_dim * sizeof(float));
+        }
+        vr_attention_mha(qs, key, value, tokens, hkv, head_dim, os);
+        for (size_t k = 0; k < hkv; ++k) {
+            memcpy(out + (k * group + g) * head_dim, os + k * head_dim, head_dim * sizeof(float));
+        }
+    }
+    free(qs);
+    free(os);
+}
+
+/* ---- int3 KV codec through the reference's contiguous cache ---- */
+int vr_int3_append_and_dump(const float* key_tokens, const float* value_tokens, size_t tokens,
+                            size_t heads, size_t head_dim, size_t block_size, uint8_t* out_kq,
+                            float* out_ks, float* out_kmirror) {
+    float* kb = (float*)calloc(tokens * heads * head_dim, sizeof(float));
+    float* vb = (float*)calloc(tokens * heads * head_dim, sizeof(float));
+    VspecKVCache cache;
+    int ok = kb && vb && vspec_kv_cache_init(&cache, kb, vb, tokens, heads, head_dim) &&
+             vspec_kv_cache_enable_int3_compression(&cache, block_size);
+    if (ok) {
+        for (size_t t = 0; t < tokens; ++t) {
+            vspec_kv_cache_append(&cache, key_tokens + t * heads * head_dim,
+                                  value_tokens + t * heads * head_dim);
+        }
+        memcpy(out_kq, cache.key_int3, tokens * heads * cache.packed_head_bytes);
+        memcpy(out_ks, cache.key_scales, tokens * heads * cache.blocks_per_head * sizeof(float));
+        memcpy(out_kmirror, kb, tokens * heads * head_dim * sizeof(float));
+        vspec_kv_cache_disable_int3_compression(&cache);
+    }
+    free(kb);
+    free(vb);
+    return ok;
+}
+
+/* Monotonic clock for the CPU baseline (CLOCK_MONOTONIC, seconds). */
+double vr_now(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
