@@ -1,0 +1,137 @@
+/*
+ * vspec_rocm.h -- C-ABI of the MI355X (gfx950) paged KV-cache decode path.
+ *
+ * Plain C: device pointers, sizes and a hipStream_t passed as void*.  No C++ or
+ * torch types cross this boundary.  Conventions follow the reference:
+ *   - cache operations return 1 on success and 0 on failure (kv_paged_cache.c);
+ *     the reason is kept per thread and read with vspec_rocm_last_error();
+ *   - the caller owns every buffer; nothing is retained past a call except the
+ *     pools made by vspec_rocm_kv_pool_create;
+ *   - no internal locking: calls that touch one pool are serialised by the caller
+ *     (one stream per pool), as the reference's structs are unsynchronised.
+ *
+ * HBM layout (decision D6), element (block b, kv head h, slot s, dim d):
+ *   f32 / f16 pools   data[((b*H + h)*P + s)*D + d]
+ *   int4 pools        codes byte ((b*H + h)*P + s)*(D/2) + d/2, nibble d&1 (even = low);
+ *                     scale  ((b*H + h)*P + s)*(D/32) + d/32, fp16 bits
+ * so one (block, head) tile of P tokens is contiguous (4 KB at P=16, D=128, f16).
+ *
+ * int4 codec (decision D1): per (token, kv head) groups of 32 elements;
+ *   rep   = 2nd-largest |x| of the group (kv_cache.c:32-59, percentile 99.5 at n=32)
+ *   scale = rep > 0 ? rep/8 : 1, floored at 1e-6, rounded to fp16 (RNE, max 65504)
+ *   code  = clip(rint(x / float(scale16)), -8, 7) with saturation (NaN -> -8)
+ *   value = code * float(scale16)                 (exact in fp32)
+ *
+ * Attention numerics follow attention_ref.c:7-88 (decision D4): q and every k are
+ * clipped to +-max(1e-6, alpha*std) (three_bit_runtime_modules.c:175-203); with
+ * VSPEC_NUMERICS_3BIT also to +-16 (:138-173), logits to +-24 (:205-250) and the
+ * scale to [1e-4, 32] (:344-361).  GQA maps query head h to kv head h / (Hq/Hkv)
+ * (runtime_inference.py:151).
+ */
+#ifndef VSPEC_ROCM_H
+#define VSPEC_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "vspec_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { VSPEC_KV_F32 = 0, VSPEC_KV_F16 = 1, VSPEC_KV_INT4 = 2 };
+enum { VSPEC_NUMERICS_PLAIN = 0, VSPEC_NUMERICS_3BIT = 1 };
+enum { VSPEC_GATHER_RAW = 0, VSPEC_GATHER_F32 = 1 };
+
+/* VspecKernelContext.config.flags bit: ctx->weight is a VspecPagedAttnDesc*. */
+#define VSPEC_KCTX_FLAG_PAGED ((size_t)1u)
+
+typedef struct VspecPagedKV {
+    int32_t dtype;          /* VSPEC_KV_* */
+    uint32_t num_blocks;
+    uint32_t block_tokens;  /* P: a multiple of 16 */
+    uint32_t num_kv_heads;
+    uint32_t head_dim;      /* 64 or 128 */
+    void* k_data;           /* device */
+    void* v_data;           /* device */
+    uint16_t* k_scales;     /* device, int4 only */
+    uint16_t* v_scales;     /* device, int4 only */
+} VspecPagedKV;
+
+/* ---- pools: hipMalloc-backed, replaces the host malloc of capi.c:2188-2219 ---- */
+size_t vspec_rocm_kv_pool_bytes(int32_t dtype, uint32_t num_blocks, uint32_t block_tokens,
+                                uint32_t num_kv_heads, uint32_t head_dim);
+int vspec_rocm_kv_pool_create(VspecPagedKV* kv, int32_t dtype, uint32_t num_blocks,
+                              uint32_t block_tokens, uint32_t num_kv_heads, uint32_t head_dim);
+void vspec_rocm_kv_pool_destroy(VspecPagedKV* kv);
+
+/* ---- append: vspec_kv_paged_append (kv_paged_cache.c:243-310) for a batch ----
+ * Writes n_new tokens per sequence at logical positions start_pos[b] .. +n_new-1
+ * through the block table.  k_new / v_new: device [batch][n_new][H][D] in src_dtype
+ * (VSPEC_KV_F32 or VSPEC_KV_F16).  An int4 pool quantises on write (D1).
+ * block_tables: device int32 [batch][max_blocks_per_seq]; start_pos: device int32 [batch]. */
+int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                         uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                         const void* k_new, const void* v_new, int32_t src_dtype, void* stream);
+
+/* ---- gather: vspec_py_kv_cache_read (capi.c:2263-2299) for a batch ----
+ * Sequence b's tokens 0..ctx_lens[b]-1 go to output tokens out_token_offset[b]+t in
+ * [T][H][D] order.  out_mode VSPEC_GATHER_RAW copies the pool format (f32, f16, or
+ * int4 codes [T][H][D/2] plus scales [T][H][D/32]); VSPEC_GATHER_F32 dequantises.
+ * max_ctx_len (host) bounds ctx_lens and sizes the grid. */
+int vspec_rocm_kv_gather(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                         uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                         uint32_t max_ctx_len, const int64_t* out_token_offset, int32_t out_mode,
+                         void* out_k, void* out_v, uint16_t* out_k_scales,
+                         uint16_t* out_v_scales, void* stream);
+
+/* ---- compaction: copy whole physical blocks (all heads, data and scales) ----
+ * dst_blocks[i] <- src_blocks[i]; device int32 arrays.  The destination set must
+ * not intersect the source set (moves run in parallel). */
+int vspec_rocm_kv_compact(const VspecPagedKV* kv, uint32_t n, const int32_t* src_blocks,
+                          const int32_t* dst_blocks, void* stream);
+
+/* ---- single-query GQA decode attention over the paged cache ---- */
+typedef struct VspecPagedAttnDesc {
+    VspecPagedKV kv;
+    uint32_t batch;
+    uint32_t num_q_heads;            /* multiple of kv.num_kv_heads */
+    const int32_t* block_tables;     /* device [batch][max_blocks_per_seq] */
+    uint32_t max_blocks_per_seq;
+    const int32_t* ctx_lens;         /* device [batch] */
+    uint32_t max_ctx_len;            /* host upper bound of ctx_lens (grid sizing) */
+    const float* q;                  /* device [batch][Hq][D] f32 */
+    float* out;                      /* device [batch][Hq][D] f32 (ctx 0 -> zeros) */
+    float scale;                     /* <= 0: 1/sqrtf(D) */
+    int32_t numerics;                /* VSPEC_NUMERICS_PLAIN or VSPEC_NUMERICS_3BIT */
+    float clamp_alpha;               /* <= 0: 4.5 */
+    uint32_t partition_tokens;       /* split-K partition length, multiple of 16; 0: auto */
+    void* workspace;                 /* device scratch or NULL (library-managed) */
+    size_t workspace_bytes;
+    void* stream;                    /* hipStream_t or NULL */
+} VspecPagedAttnDesc;
+
+size_t vspec_rocm_paged_decode_workspace_bytes(const VspecPagedAttnDesc* desc);
+int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc);
+
+/* ---- misc ---- */
+int vspec_rocm_sync(void* stream);
+const char* vspec_rocm_last_error(void);
+int vspec_rocm_device_count(void);
+
+/* ---- backend registry entry: replaces rocm_backend_stub.c:3-21 ----
+ * launch_attention accepts either the reference context (ctx->input host q [H][D],
+ * ctx->weight const VspecKVCache*, ctx->output host out [H][D]; cpu_backend.c:40-51)
+ * or, with VSPEC_KCTX_FLAG_PAGED in ctx->config.flags, a VspecPagedAttnDesc* in
+ * ctx->weight (device pointers).  launch_linear is out of scope and is a no-op that
+ * records an error, like the stub it replaces.  Bad arguments are silent no-ops,
+ * as in the reference, with the reason in vspec_rocm_last_error(). */
+int vspec_rocm_backend_available(void);
+VspecBackend vspec_make_rocm_backend(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -267,6 +267,7 @@ class Reference:
             "vr_attention_gqa": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _f32p]),
             "vr_int3_append_and_dump": (C.c_int, [_f32p, _f32p, _sz, _sz, _sz, _sz, _u8p, _f32p, _f32p]),
             "vr_now": (C.c_double, []),
+            "vr_baseline_decode": (C.c_double, [C.c_int, _sz, _sz, _sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p]),
             "vspec_kv_paged_open_session": (C.c_int, [_vp, C.c_uint64]),
             "vspec_kv_paged_close_session": (C.c_int, [_vp, C.c_uint64]),
             "vspec_kv_paged_reuse_prefix": (C.c_int, [_vp, C.c_uint64, C.c_uint64, _sz]),
@@ -299,6 +300,22 @@ class Reference:
             os.environ["VSPEC_3BIT_RUNTIME_MODULE"] = "1"
         else:
             os.environ.pop("VSPEC_3BIT_RUNTIME_MODULE", None)
+
+    def baseline_decode(self, mode, nthreads, k, v, q, block_tokens=16):
+        """Time the reference decode step (append + capi gather + GQA attention_ref) over
+        sequences k, v [S][T][Hkv][D] f32, q [S][Hq][D].  Returns (seconds, out)."""
+        self.set_mode(mode)
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        q = np.ascontiguousarray(q, np.float32)
+        S, T, Hkv, D = k.shape
+        Hq = q.shape[1]
+        out = np.zeros((S, Hq, D), np.float32)
+        sec = self.lib.vr_baseline_decode(nthreads, S, T, Hq, Hkv, D, block_tokens, ptr(k, _f32p), ptr(v, _f32p),
+                                          ptr(q, _f32p), ptr(out, _f32p))
+        if sec < 0:
+            raise RuntimeError("reference baseline failed")
+        return sec, out
 
     def attention_mha(self, mode, q, k, v):
         self.set_mode(mode)

@@ -174,3 +174,94 @@ double vr_now(void) {
     clock_gettime(CLOCK_MONOTONIC, &ts);
     return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
 }
+
+/* ---- CPU baseline: the reference decode step for a batch of sequences ----
+ * Per sequence (the reference's own path, one layer):
+ *   setup (untimed): a fresh paged cache with T-1 tokens appended
+ *   timed: append the decode-step token (kv_paged_cache.c:243-310), gather all T
+ *          tokens through get_token_ptr (capi.c:2263-2299 loop), then GQA
+ *          attention_ref (cpu_backend.c:40-51 per head group).
+ * Sequences are split over nthreads POSIX threads.  Returns the timed wall seconds. */
+#include <pthread.h>
+
+typedef struct VrJob {
+    size_t first, last, T, hq, hkv, d, p;
+    const float *k, *v, *q;
+    float* out;
+    VspecKVPagedCache** caches;
+    float *gk, *gv; /* per-thread gather buffers */
+    int ok;
+} VrJob;
+
+static void* vr_job_setup(void* arg) {
+    VrJob* j = (VrJob*)arg;
+    const size_t row = j->hkv * j->d;
+    for (size_t s = j->first; s < j->last; ++s) {
+        VspecKVPagedCache* c = vr_paged_new(j->p, (j->T + j->p - 1) / j->p, j->hkv, j->d);
+        j->caches[s] = c;
+        if (!c) { j->ok = 0; return NULL; }
+        const float* ks = j->k + s * j->T * row;
+        const float* vs = j->v + s * j->T * row;
+        for (size_t t = 0; t + 1 < j->T; ++t) {
+            if (!vspec_kv_paged_append(c, 1u, ks + t * row, vs + t * row)) { j->ok = 0; return NULL; }
+        }
+    }
+    return NULL;
+}
+
+static void* vr_job_run(void* arg) {
+    VrJob* j = (VrJob*)arg;
+    const size_t row = j->hkv * j->d;
+    for (size_t s = j->first; s < j->last; ++s) {
+        VspecKVPagedCache* c = j->caches[s];
+        const size_t t = j->T - 1;
+        if (!vspec_kv_paged_append(c, 1u, j->k + (s * j->T + t) * row, j->v + (s * j->T + t) * row)) {
+            j->ok = 0;
+            return NULL;
+        }
+        if (vr_paged_read(c, 1u, j->gk, j->gv, 0) != j->T) { j->ok = 0; return NULL; }
+        vr_attention_gqa(j->q + s * j->hq * j->d, j->gk, j->gv, j->T, j->hq, j->hkv, j->d,
+                         j->out + s * j->hq * j->d);
+    }
+    return NULL;
+}
+
+double vr_baseline_decode(int nthreads, size_t nseq, size_t T, size_t hq, size_t hkv, size_t d,
+                          size_t p, const float* k, const float* v, const float* q, float* out) {
+    if (nthreads < 1) nthreads = 1;
+    if ((size_t)nthreads > nseq) nthreads = (int)nseq;
+    VspecKVPagedCache** caches = (VspecKVPagedCache**)calloc(nseq, sizeof(*caches));
+    VrJob* jobs = (VrJob*)calloc((size_t)nthreads, sizeof(VrJob));
+    pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+    double elapsed = -1.0;
+    int ok = caches && jobs && th;
+    for (int i = 0; ok && i < nthreads; ++i) {
+        VrJob* j = &jobs[i];
+        j->first = nseq * (size_t)i / (size_t)nthreads;
+        j->last = nseq * (size_t)(i + 1) / (size_t)nthreads;
+        j->T = T; j->hq = hq; j->hkv = hkv; j->d = d; j->p = p;
+        j->k = k; j->v = v; j->q = q; j->out = out; j->caches = caches; j->ok = 1;
+        j->gk = (float*)malloc(T * hkv * d * sizeof(float));
+        j->gv = (float*)malloc(T * hkv * d * sizeof(float));
+        if (!j->gk || !j->gv) ok = 0;
+    }
+    if (ok) {
+        for (int i = 0; i < nthreads; ++i) pthread_create(&th[i], NULL, vr_job_setup, &jobs[i]);
+        for (int i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
+        for (int i = 0; i < nthreads; ++i) ok = ok && jobs[i].ok;
+    }
+    if (ok) {
+        const double t0 = vr_now();
+        for (int i = 0; i < nthreads; ++i) pthread_create(&th[i], NULL, vr_job_run, &jobs[i]);
+        for (int i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
+        elapsed = vr_now() - t0;
+        for (int i = 0; i < nthreads; ++i) ok = ok && jobs[i].ok;
+        if (!ok) elapsed = -1.0;
+    }
+    for (size_t s = 0; caches && s < nseq; ++s) vr_paged_free(caches[s]);
+    for (int i = 0; jobs && i < nthreads; ++i) { free(jobs[i].gk); free(jobs[i].gv); }
+    free(caches);
+    free(jobs);
+    free(th);
+    return elapsed;
+}

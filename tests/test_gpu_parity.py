@@ -1,0 +1,299 @@
+"""GPU parity: the HIP path (through the C-ABI) against the CPU oracle on the same
+seeded inputs.
+
+Bars:
+  * append, gather, compaction and int4 codes/scales: bit-exact;
+  * attention: max-abs 1e-4 with fp32 KV, 4e-3 with fp16 / int4 KV (fp32 accumulate),
+    in both reference numerics modes (P: 3-bit module off, R: on).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle.oracle import DTYPE_F16, DTYPE_F32, DTYPE_INT4, HostPool
+from cases import GARBAGE, continuous_c4, make_case, qwen_c2
+
+pytestmark = pytest.mark.gpu
+TOL = {DTYPE_F32: 1e-4, DTYPE_F16: 4e-3, DTYPE_INT4: 4e-3}
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    import torch
+    import vspec_rocm
+
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible for a gpu-marked test")
+    vspec_rocm.lib()
+    return torch.device("cuda:0")
+
+
+def _np_to_dev(a, dev):
+    import torch
+
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16).copy()).view(torch.float16).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def device_pool(case, dev):
+    import torch
+    import vspec_rocm as vr
+
+    pool = vr.PagedPool(case.dtype, case.num_blocks, case.P, case.Hkv, case.D, device=dev)
+    g, gs = GARBAGE[case.dtype]
+    if case.dtype == DTYPE_F32:
+        pool.k.view(torch.int32).fill_(int(np.int32(np.uint32(g).view(np.int32))))
+        pool.v.view(torch.int32).fill_(int(np.int32(np.uint32(g).view(np.int32))))
+    elif case.dtype == DTYPE_F16:
+        pool.k.view(torch.int16).fill_(int(np.uint16(g).view(np.int16)))
+        pool.v.view(torch.int16).fill_(int(np.uint16(g).view(np.int16)))
+    else:
+        pool.k.fill_(int(g))
+        pool.v.fill_(int(g))
+        pool.ks.fill_(int(np.uint16(gs).view(np.int16)))
+        pool.vs.fill_(int(np.uint16(gs).view(np.int16)))
+    return pool
+
+
+def pool_bytes(pool):
+    """Device pool -> numpy views comparable with HostPool arrays."""
+    import torch
+
+    def cv(t, like):
+        if t is None:
+            return None
+        if t.dtype == torch.float16:
+            return t.view(torch.int16).cpu().numpy().view(np.uint16)
+        if t.dtype == torch.int16:
+            return t.cpu().numpy().view(np.uint16)
+        return t.cpu().numpy()
+
+    return [cv(pool.k, None), cv(pool.v, None), cv(pool.ks, None), cv(pool.vs, None)]
+
+
+def assert_pools_equal(host: HostPool, pool):
+    got = pool_bytes(pool)
+    want = [host.k, host.v, host.ks, host.vs]
+    for name, g, w in zip(("k", "v", "k_scales", "v_scales"), got, want):
+        if w is None:
+            assert g is None
+            continue
+        g = np.ascontiguousarray(g).view(np.uint8)
+        w = np.ascontiguousarray(w).view(np.uint8)
+        bad = np.flatnonzero(g != w)
+        assert bad.size == 0, f"{name}: {bad.size} bytes differ, first at {bad[:8]}"
+
+
+def build_both(oracle, case, dev, prefix_split=True):
+    """Append the case's token stream on both sides: context minus one token as one
+    chunk, then the decode-step token."""
+    import torch
+    import vspec_rocm as vr
+
+    pool = device_pool(case, dev)
+    tab_d = torch.from_numpy(case.tables).to(dev)
+    B, T = case.B, case.tmax
+    # per-sequence streams are written up to their own ctx: append in uniform chunks
+    # over the prefix every sequence shares, then token-by-token for ragged tails
+    tmin = int(case.ctx.min())
+    first = tmin - 1 if prefix_split and tmin > 1 else tmin
+    k_d = _np_to_dev(case.k_tokens, dev)
+    v_d = _np_to_dev(case.v_tokens, dev)
+    if first > 0:
+        kk = np.ascontiguousarray(case.k_tokens[:, :first])
+        vv = np.ascontiguousarray(case.v_tokens[:, :first])
+        assert oracle.paged_append(case.host, case.tables, np.zeros(B, np.int32), kk, vv)
+        vr.kv_append(pool, tab_d, torch.zeros(B, dtype=torch.int32, device=dev),
+                     k_d[:, :first].contiguous(), v_d[:, :first].contiguous())
+    for t in range(first, T):
+        live = np.flatnonzero(case.ctx > t)
+        if live.size == 0:
+            continue
+        kk = np.ascontiguousarray(case.k_tokens[live, t:t + 1])
+        vv = np.ascontiguousarray(case.v_tokens[live, t:t + 1])
+        sp = np.full(live.size, t, np.int32)
+        tabs = np.ascontiguousarray(case.tables[live])
+        assert oracle.paged_append(case.host, tabs, sp, kk, vv)
+        li = torch.from_numpy(live).to(dev)
+        vr.kv_append(pool, torch.from_numpy(tabs).to(dev), torch.from_numpy(sp).to(dev),
+                     k_d[li, t:t + 1].contiguous(), v_d[li, t:t + 1].contiguous())
+    torch.cuda.synchronize()
+    return pool
+
+
+def run_decode(case, pool, dev, mode, partition_tokens=0):
+    import torch
+    import vspec_rocm as vr
+
+    q = torch.from_numpy(case.q).to(dev)
+    out = vr.paged_decode(pool, torch.from_numpy(case.tables).to(dev), torch.from_numpy(case.ctx).to(dev), q,
+                          max_ctx_len=case.tmax, numerics=mode, partition_tokens=partition_tokens)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def check_attention(oracle, case, got, mode, subset=None):
+    idx = np.arange(case.B) if subset is None else np.asarray(subset)
+    want = oracle.paged_decode(mode, case.host, case.tables[idx], case.ctx[idx], case.q[idx])
+    err = np.abs(got[idx] - want)
+    assert np.isfinite(got[idx]).all()
+    tol = TOL[case.dtype]
+    assert err.max() <= tol, f"max-abs {err.max():.3e} > {tol:.0e} (mode {mode})"
+    return float(err.max())
+
+
+# ----------------------------------------------------------------------------- config 1
+@pytest.mark.parametrize("mode", [0, 1])
+def test_config1_cpu_reference_shape(oracle, gpu, mode):
+    """C1: 1 sequence, MHA 8x64, 256 cached + 1 appended token, P=16, identity table,
+    fp32 K/V/Q ~ N(0,1)."""
+    say(f"[c1] mode={mode} build")
+    case = make_case(oracle, DTYPE_F32, 1, 8, 8, 64, 16, [257], seed=1, table="identity")
+    pool = build_both(oracle, case, gpu)
+    assert_pools_equal(case.host, pool)
+    say("[c1] gather")
+    import torch
+    import vspec_rocm as vr
+
+    gk, gv, _, _ = vr.kv_gather(pool, torch.from_numpy(case.tables).to(gpu), torch.from_numpy(case.ctx).to(gpu))
+    ok_, ov, _, _ = oracle.paged_gather(case.host, case.tables, case.ctx)
+    assert np.array_equal(gk.cpu().numpy().view(np.uint32), ok_.view(np.uint32))
+    assert np.array_equal(gv.cpu().numpy().view(np.uint32), ov.view(np.uint32))
+    assert np.array_equal(ok_.reshape(257, 8, 64), case.k_tokens[0])
+    say("[c1] decode")
+    got = run_decode(case, pool, gpu, mode)
+    check_attention(oracle, case, got, mode)
+
+
+# ----------------------------------------------------------------------------- append / gather
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+@pytest.mark.parametrize("src16", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+def test_append_gather_bitexact(oracle, gpu, dtype, src16, D):
+    import torch
+    import vspec_rocm as vr
+
+    say(f"[append] dtype={dtype} src16={src16} D={D}")
+    case = make_case(oracle, dtype, 3, 4, 2, D, 32, [45, 1, 70], seed=10 + dtype + 3 * src16 + D,
+                     num_blocks=9, src16=src16)
+    # tiny and huge values exercise fp16 subnormals/overflow and the int4 scale floor
+    case.k_tokens = case.k_tokens.copy()
+    if not src16:
+        case.k_tokens[0, 3, 0, :5] = [1e-8, -3e-7, 7e4, -1e5, 6.1e-5]
+        case.k_tokens[2, 5, 1, :] = 1e-9
+    pool = build_both(oracle, case, gpu)
+    assert_pools_equal(case.host, pool)
+    tab = torch.from_numpy(case.tables).to(gpu)
+    ctx = torch.from_numpy(case.ctx).to(gpu)
+    for mode in (0, 1):
+        say(f"[gather] dtype={dtype} out_mode={mode}")
+        gk, gv, gks, gvs = vr.kv_gather(pool, tab, ctx, out_mode=mode)
+        wk, wv, wks, wvs = oracle.paged_gather(case.host, case.tables, case.ctx, out_mode=mode)
+        for g, w in ((gk, wk), (gv, wv), (gks, wks), (gvs, wvs)):
+            if w is None:
+                continue
+            gb = g.cpu().numpy().view(np.uint8)
+            assert np.array_equal(gb, np.ascontiguousarray(w).view(np.uint8))
+
+
+def test_compact_bitexact(oracle, gpu):
+    import torch
+    import vspec_rocm as vr
+
+    say("[compact]")
+    case = make_case(oracle, DTYPE_INT4, 2, 8, 2, 128, 16, [80, 50], seed=77, num_blocks=16)
+    pool = build_both(oracle, case, gpu)
+    src = np.concatenate([case.tables[0, 1:5], case.tables[1, 1:4]]).astype(np.int32)
+    used = set(case.tables[case.tables >= 0].tolist())
+    free = np.array([b for b in range(16) if b not in used], np.int32)
+    assert free.size >= src.size
+    dst = free[: src.size]
+    assert oracle.paged_compact(case.host, src, dst)
+    vr.kv_compact(pool, torch.from_numpy(src).to(gpu), torch.from_numpy(dst).to(gpu))
+    torch.cuda.synchronize()
+    assert_pools_equal(case.host, pool)
+
+
+# ----------------------------------------------------------------------------- decode edge cases
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 8), (128, 8, 4), (128, 16, 4), (128, 16, 2), (64, 6, 2)])
+def test_decode_edges(oracle, gpu, dtype, D, Hq, Hkv):
+    """Ragged contexts around tile/block edges, GQA groups 1/2/3/4/8, garbage (NaN)
+    beyond each context, several partition sizes."""
+    ctx = [1, 15, 16, 17, 33, 64, 100, 0]
+    say(f"[edges] dtype={dtype} D={D} Hq={Hq} Hkv={Hkv}")
+    case = make_case(oracle, dtype, len(ctx), Hq, Hkv, D, 32, ctx, seed=5 * D + Hq + dtype,
+                     num_blocks=20)
+    pool = build_both(oracle, case, gpu)
+    for mode in (0, 1):
+        for pt in (0, 16, 48):
+            say(f"[edges] mode={mode} partition_tokens={pt}")
+            got = run_decode(case, pool, gpu, mode, partition_tokens=pt)
+            assert np.all(got[-1] == 0.0)  # empty context -> zeros
+            check_attention(oracle, case, got, mode, subset=range(len(ctx) - 1))
+
+
+def test_decode_outliers_fire_clamp(oracle, gpu):
+    """Large outliers make the std-clamp (and in mode R the +-16 clip and +-24 logit
+    clip) change the result; the GPU must follow the reference there too."""
+    say("[outliers]")
+    case = make_case(oracle, DTYPE_F32, 2, 8, 2, 128, 16, [300, 77], seed=91)
+    k = case.k_tokens.copy()
+    k[0, ::7, 0, 3] = 40.0
+    k[1, ::5, 1, 100] = -25.0
+    k[0, 10, 1, :] *= 20.0
+    case.k_tokens = k
+    case.q = case.q.copy()
+    case.q[0, 0, 7] = 30.0
+    case.q[1] *= 8.0
+    pool = build_both(oracle, case, gpu)
+    for mode in (0, 1):
+        got = run_decode(case, pool, gpu, mode)
+        check_attention(oracle, case, got, mode)
+
+
+# ----------------------------------------------------------------------------- configs 2-4
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_config2_3_qwen_decode(oracle, gpu, dtype, mode):
+    """C2 (fp16) and C3 (int4 quantize-on-write): B=16, GQA 32/8, D=128, T=2048+1."""
+    say(f"[c2/c3] dtype={dtype} mode={mode} build")
+    case = qwen_c2(oracle, dtype)
+    pool = build_both(oracle, case, gpu)
+    assert_pools_equal(case.host, pool)
+    say(f"[c2/c3] dtype={dtype} mode={mode} decode")
+    got = run_decode(case, pool, gpu, mode)
+    err = check_attention(oracle, case, got, mode)
+    say(f"[c2/c3] max-abs {err:.2e}")
+
+
+def test_config4_continuous_batching(oracle, gpu):
+    """C4: B=64, context ~ U[128, 8192], fragmented tables from a 1.2x pool (fp16).
+    The oracle checks 12 sequences including the shortest and the longest."""
+    say("[c4] build")
+    case = continuous_c4(oracle)
+    pool = build_both(oracle, case, gpu, prefix_split=False)
+    order = np.argsort(case.ctx)
+    subset = sorted(set(order[:4].tolist() + order[-4:].tolist() + [0, 1, 31, 63]))
+    for pt in (0, 256):
+        say(f"[c4] decode partition_tokens={pt}")
+        got = run_decode(case, pool, gpu, 0, partition_tokens=pt)
+        check_attention(oracle, case, got, 0, subset=subset)
+
+
+def test_decode_partition_invariance(oracle, gpu):
+    """Split-K partition size changes rounding only."""
+    say("[partitions]")
+    case = make_case(oracle, DTYPE_F16, 4, 32, 8, 128, 16, [1000, 2049, 17, 513], seed=33)
+    pool = build_both(oracle, case, gpu)
+    outs = [run_decode(case, pool, gpu, 0, partition_tokens=pt) for pt in (0, 16, 64, 256, 4096)]
+    for o in outs[1:]:
+        assert np.abs(o - outs[0]).max() < 1e-5
+    check_attention(oracle, case, outs[0], 0)

@@ -1,0 +1,1152 @@
+// paged_kv.hip -- gfx950 kernels and C-ABI for the Vspec paged KV-cache decode path.
+//
+// Kernels (all wave64):
+//   kv_append      block-table append of new K/V; int4 pools quantise on write
+//   kv_gather      block-table gather into [T][H][D] (raw bytes or dequantised f32)
+//   kv_compact     whole-block moves (compaction after eviction)
+//   decode_partial single-query GQA attention, split-K over 16-token tiles
+//   decode_combine log-sum-exp merge of the split-K partials
+//
+// The C-ABI is declared in include/vspec_rocm.h.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "vspec_rocm.h"
+
+// ---------------------------------------------------------------------------
+// error reporting
+// ---------------------------------------------------------------------------
+namespace {
+thread_local char g_err[512] = "";
+
+void set_err(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+}  // namespace
+
+extern "C" void vspec_rocm_set_error_(const char* msg) { set_err("%s", msg ? msg : ""); }
+
+#define HIP_CHECK(call, what)                                              \
+    do {                                                                   \
+        hipError_t e_ = (call);                                            \
+        if (e_ != hipSuccess) {                                            \
+            set_err("%s: %s", (what), hipGetErrorString(e_));              \
+            return 0;                                                      \
+        }                                                                  \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kTile = 16;   // tokens per attention tile
+constexpr int kWaves = 4;   // waves per attention workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+
+__device__ __forceinline__ uint32_t float_to_half_bits(float x) {
+    // v_cvt_f16_f32 under the default round-to-nearest-even mode
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x)));
+}
+
+__device__ __forceinline__ void unpack_f16x8(const uint4 w, float* out) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        out[2 * i] = half_bits_to_float(ws[i] & 0xffffu);
+        out[2 * i + 1] = half_bits_to_float(ws[i] >> 16);
+    }
+}
+
+// signed nibble i (0..7) of a 32-bit word, even element in the low nibble
+__device__ __forceinline__ float nibble(uint32_t w, int i) {
+    return static_cast<float>(static_cast<int32_t>(w << (28 - 4 * i)) >> 28);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// DPP controls
+constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+// Sum over aligned groups of N lanes (N = 4, 8, 16); every lane gets the total.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(N == 4 || N == 8 || N == 16, "group size");
+    x += dpp<kQuadXor1>(x);
+    x += dpp<kQuadXor2>(x);
+    if constexpr (N >= 8) x += dpp<kRowHalfMirror>(x);
+    if constexpr (N >= 16) x += dpp<kRowMirror>(x);
+    return x;
+}
+
+// Max over the 64/N groups of a wave when x is uniform inside each aligned group of N.
+template <int N>
+__device__ __forceinline__ float max_across_groups(float x) {
+    if constexpr (N <= 4) x = fmaxf(x, dpp<kRowHalfMirror>(x));
+    if constexpr (N <= 8) x = fmaxf(x, dpp<kRowMirror>(x));
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+
+// ---------------------------------------------------------------------------
+// decode attention
+// ---------------------------------------------------------------------------
+struct DecodeParams {
+    const uint8_t* k;
+    const uint8_t* v;
+    const uint16_t* ks;
+    const uint16_t* vs;
+    const int32_t* block_tables;
+    const int32_t* ctx_lens;
+    const float* q;
+    float* out;
+    float* part_ml;    // [B][Hq][max_parts][2] (max in log2 units, sum)
+    float* part_acc;   // [B][Hq][max_parts][D]
+    uint32_t hq;
+    uint32_t hkv;
+    uint32_t block_tokens;
+    uint32_t max_blocks;
+    uint32_t num_blocks;
+    uint32_t tiles_per_part;
+    uint32_t max_parts;
+    uint32_t gsplit;   // work items per kv head (Hq/Hkv/GW)
+    float qscale;      // softmax scale * log2(e)
+    float alpha;       // std-clamp alpha
+    float logit_clip;  // +-24*log2(e) in 3-bit mode, +inf otherwise
+    float input_clip;  // 16 in 3-bit mode, +inf otherwise
+};
+
+// Per-dtype geometry of one row (one token of one kv head).
+template <int DT, int D>
+struct Row {
+    static constexpr int kBytes = DT == VSPEC_KV_F32 ? D * 4 : (DT == VSPEC_KV_F16 ? D * 2 : D / 2);
+    static constexpr int kScales = DT == VSPEC_KV_INT4 ? D / 32 : 0;
+};
+
+// K-side layout: LPK lanes hold one key, 16 elements per lane.
+//   f16:  chunks of 8 elements (16 B), lane chunks sub, sub+LPK
+//   f32:  chunks of 4 elements (16 B), lane chunks sub + j*LPK, j < 4
+//   int4: 16 consecutive elements (8 B of codes), one scale
+template <int DT, int D>
+__device__ __forceinline__ int k_elem(int sub, int e) {
+    constexpr int LPK = D / 16;
+    if constexpr (DT == VSPEC_KV_F16) {
+        return 8 * (sub + (e / 8) * LPK) + (e % 8);
+    } else if constexpr (DT == VSPEC_KV_F32) {
+        return 4 * (sub + (e / 4) * LPK) + (e % 4);
+    } else {
+        return 16 * sub + e;
+    }
+}
+
+template <int DT, int D>
+__device__ __forceinline__ void load_k16(const DecodeParams& p, size_t row, int sub, float* x) {
+    constexpr int LPK = D / 16;
+    if constexpr (DT == VSPEC_KV_F16) {
+        const uint4* src = reinterpret_cast<const uint4*>(p.k + row * (size_t)(D * 2));
+        unpack_f16x8(src[sub], x);
+        unpack_f16x8(src[sub + LPK], x + 8);
+    } else if constexpr (DT == VSPEC_KV_F32) {
+        const float4* src = reinterpret_cast<const float4*>(p.k + row * (size_t)(D * 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 w = src[sub + j * LPK];
+            x[4 * j] = w.x;
+            x[4 * j + 1] = w.y;
+            x[4 * j + 2] = w.z;
+            x[4 * j + 3] = w.w;
+        }
+    } else {
+        const uint2 w = reinterpret_cast<const uint2*>(p.k + row * (size_t)(D / 2))[sub];
+        const float sc = half_bits_to_float(p.ks[row * (size_t)(D / 32) + sub / 2]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[i] = nibble(w.x, i) * sc;
+            x[8 + i] = nibble(w.y, i) * sc;
+        }
+    }
+}
+
+// V-side layout: D/8 lanes per token, lane chunk c holds elements 8c..8c+7.
+template <int DT, int D>
+__device__ __forceinline__ void load_v8(const DecodeParams& p, size_t row, int c, float* x) {
+    if constexpr (DT == VSPEC_KV_F16) {
+        const uint4 w = reinterpret_cast<const uint4*>(p.v + row * (size_t)(D * 2))[c];
+        unpack_f16x8(w, x);
+    } else if constexpr (DT == VSPEC_KV_F32) {
+        const float4* src = reinterpret_cast<const float4*>(p.v + row * (size_t)(D * 4));
+        const float4 a = src[2 * c];
+        const float4 b = src[2 * c + 1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+        const uint32_t w = reinterpret_cast<const uint32_t*>(p.v + row * (size_t)(D / 2))[c];
+        const float sc = half_bits_to_float(p.vs[row * (size_t)(D / 32) + c / 4]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = nibble(w, i) * sc;
+    }
+}
+
+// Clip a row held by LPK lanes (16 elements each) to +-max(1e-6, alpha*std),
+// then to +-input_clip (three_bit_runtime_modules.c:175-203, :138-173).
+template <int LPK, int D>
+__device__ __forceinline__ void clamp_row(float* x, float alpha, float input_clip) {
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += x[e];
+    const float mean = group_sum<LPK>(s) * (1.0f / D);
+    float v = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const float d = x[e] - mean;
+        v = fmaf(d, d, v);
+    }
+    const float var = group_sum<LPK>(v) * (1.0f / D);
+    const float th = fminf(fmaxf(1e-6f, alpha * sqrtf(var)), input_clip);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) x[e] = fminf(fmaxf(x[e], -th), th);
+}
+
+template <int DT, int D, int GW>
+__global__ __launch_bounds__(256, 2) void decode_partial(DecodeParams p) {
+    constexpr int LPK = D / 16;           // lanes per key
+    constexpr int KPP = 64 / LPK;         // keys per K pass
+    constexpr int KPASS = kTile / KPP;    // K passes per tile
+    constexpr int VLPT = D / 8;           // lanes per token on the V side
+    constexpr int VTPP = 64 / VLPT;       // tokens per V pass
+    constexpr int VPASS = kTile / VTPP;   // V passes per tile
+    static_assert(KPASS >= 1 && VPASS >= 1, "tile geometry");
+
+    __shared__ float p_lds[kWaves][2][kTile][GW];
+    __shared__ float comb[kWaves][GW][D + 2];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int part = blockIdx.x;
+    const int b = blockIdx.z;
+    const int hk = blockIdx.y / p.gsplit;
+    const int hq0 = hk * (p.gsplit * GW) + (blockIdx.y % p.gsplit) * GW;
+
+    // tiles beyond the block table or the planned partitions are never read
+    const int tiles_per_block = (int)p.block_tokens / kTile;
+    const int ctx = min(max(p.ctx_lens[b], 0), (int)(p.max_blocks * p.block_tokens));
+    const int ntiles = min((ctx + kTile - 1) / kTile, (int)(p.max_parts * p.tiles_per_part));
+    const int nparts = max(1, (ntiles + (int)p.tiles_per_part - 1) / (int)p.tiles_per_part);
+    if (part >= nparts) return;
+    const int tile_begin = part * (int)p.tiles_per_part;
+    const int tile_end = min(ntiles, tile_begin + (int)p.tiles_per_part);
+
+    const int kk = lane / LPK;      // key within a K pass
+    const int sub = lane % LPK;     // lane within the key
+    const int vc = lane % VLPT;     // V chunk
+    const int vt = lane / VLPT;     // token within a V pass
+
+    // q' = clip(q) * scale * log2(e), in the K-side lane layout
+    float qv[GW][16];
+#pragma unroll
+    for (int h = 0; h < GW; ++h) {
+        const float* qrow = p.q + ((size_t)b * p.hq + hq0 + h) * D;
+        float x[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) x[e] = qrow[k_elem<DT, D>(sub, e)];
+        clamp_row<LPK, D>(x, p.alpha, p.input_clip);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) qv[h][e] = x[e] * p.qscale;
+    }
+
+    float m_run[GW], l_run[GW], acc[GW][8];
+#pragma unroll
+    for (int h = 0; h < GW; ++h) {
+        m_run[h] = -INFINITY;
+        l_run[h] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+    }
+
+    const int32_t* table = p.block_tables + (size_t)b * p.max_blocks;
+    int buf = 0;
+    for (int tile = tile_begin + wave; tile < tile_end; tile += kWaves) {
+        const int lblock = tile / tiles_per_block;
+        const int phys = table[lblock];
+        if (phys < 0 || (uint32_t)phys >= p.num_blocks) continue;  // invalid entry: tile skipped
+        const size_t row0 = ((size_t)phys * p.hkv + hk) * p.block_tokens +
+                            (size_t)(tile % tiles_per_block) * kTile;
+        const int tok0 = tile * kTile;
+
+        // ---- scores ----
+        float s[KPASS][GW];
+#pragma unroll
+        for (int kp = 0; kp < KPASS; ++kp) {
+            const int slot = kp * KPP + kk;
+            float x[16];
+            load_k16<DT, D>(p, row0 + slot, sub, x);
+            clamp_row<LPK, D>(x, p.alpha, p.input_clip);
+            const bool valid = tok0 + slot < ctx;
+#pragma unroll
+            for (int h = 0; h < GW; ++h) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) d = fmaf(qv[h][e], x[e], d);
+                d = group_sum<LPK>(d);
+                d = fminf(fmaxf(d, -p.logit_clip), p.logit_clip);
+                s[kp][h] = valid ? d : -INFINITY;
+            }
+        }
+
+        // ---- online softmax (rescale only when the max grows by > 2^8) ----
+#pragma unroll
+        for (int h = 0; h < GW; ++h) {
+            float mt = s[0][h];
+#pragma unroll
+            for (int kp = 1; kp < KPASS; ++kp) mt = fmaxf(mt, s[kp][h]);
+            mt = max_across_groups<LPK>(mt);
+            // uniform across the wave after the reduction: keep it in an SGPR
+            mt = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mt)));
+            if (mt > m_run[h] + 8.0f) {
+                const float f = exp2f(m_run[h] - mt);
+                l_run[h] *= f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] *= f;
+                m_run[h] = mt;
+            }
+        }
+#pragma unroll
+        for (int kp = 0; kp < KPASS; ++kp) {
+            if (sub < GW) {
+                float sv = s[kp][0], mv = m_run[0];
+#pragma unroll
+                for (int h = 1; h < GW; ++h) {
+                    if (sub == h) {
+                        sv = s[kp][h];
+                        mv = m_run[h];
+                    }
+                }
+                p_lds[wave][buf][kp * KPP + kk][sub] = exp2f(sv - mv);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // ---- P.V ----
+        const bool tail = tok0 + kTile > ctx;
+#pragma unroll
+        for (int vp = 0; vp < VPASS; ++vp) {
+            const int slot = vp * VTPP + vt;
+            float x[8];
+            load_v8<DT, D>(p, row0 + slot, vc, x);
+            if (tail && tok0 + slot >= ctx) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = 0.f;
+            }
+            float pv[GW];
+#pragma unroll
+            for (int h = 0; h < GW; ++h) pv[h] = p_lds[wave][buf][slot][h];
+#pragma unroll
+            for (int h = 0; h < GW; ++h) {
+                l_run[h] += pv[h];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pv[h], x[e], acc[h][e]);
+            }
+        }
+        buf ^= 1;
+    }
+
+    // ---- reduce the token groups of the V layout (lanes with equal chunk) ----
+#pragma unroll
+    for (int h = 0; h < GW; ++h) {
+#pragma unroll
+        for (int off = VLPT; off < 64; off <<= 1) {
+            l_run[h] += __shfl_xor(l_run[h], off);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
+        }
+    }
+    if (lane < VLPT) {
+#pragma unroll
+        for (int h = 0; h < GW; ++h) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) comb[wave][h][2 + 8 * vc + e] = acc[h][e];
+            if (vc == 0) {
+                comb[wave][h][0] = m_run[h];
+                comb[wave][h][1] = l_run[h];
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- merge the waves of this workgroup ----
+    for (int idx = threadIdx.x; idx < GW * D; idx += 256) {
+        const int h = idx / D;
+        const int d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[w][h][0]);
+        float a = 0.f, l = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = comb[w][h][0];
+            if (mw != -INFINITY) {
+                const float f = exp2f(mw - M);
+                a = fmaf(comb[w][h][2 + d], f, a);
+                l = fmaf(comb[w][h][1], f, l);
+            }
+        }
+        const size_t hq = (size_t)b * p.hq + hq0 + h;
+        if (nparts == 1) {
+            p.out[hq * D + d] = l > 0.f ? a / l : 0.f;
+        } else {
+            const size_t slot = hq * p.max_parts + part;
+            p.part_acc[slot * D + d] = a;
+            if (d == 0) {
+                p.part_ml[2 * slot] = M;
+                p.part_ml[2 * slot + 1] = l;
+            }
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void decode_combine(DecodeParams p) {
+    const int b = blockIdx.y;
+    const int hq = blockIdx.x;
+    const int d = threadIdx.x;
+    const int ctx = min(max(p.ctx_lens[b], 0), (int)(p.max_blocks * p.block_tokens));
+    const int ntiles = min((ctx + kTile - 1) / kTile, (int)(p.max_parts * p.tiles_per_part));
+    const int nparts = max(1, (ntiles + (int)p.tiles_per_part - 1) / (int)p.tiles_per_part);
+    if (nparts == 1) return;
+    const size_t base = ((size_t)b * p.hq + hq) * p.max_parts;
+    float M = -INFINITY;
+    for (int i = 0; i < nparts; ++i) M = fmaxf(M, p.part_ml[2 * (base + i)]);
+    float a = 0.f, l = 0.f;
+    for (int i = 0; i < nparts; ++i) {
+        const float mi = p.part_ml[2 * (base + i)];
+        if (mi != -INFINITY) {
+            const float f = exp2f(mi - M);
+            a = fmaf(p.part_acc[(base + i) * D + d], f, a);
+            l = fmaf(p.part_ml[2 * (base + i) + 1], f, l);
+        }
+    }
+    p.out[((size_t)b * p.hq + hq) * D + d] = l > 0.f ? a / l : 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// append (quantise-on-write for int4)
+// ---------------------------------------------------------------------------
+struct AppendParams {
+    uint8_t* k;
+    uint8_t* v;
+    uint16_t* ks;
+    uint16_t* vs;
+    const int32_t* block_tables;
+    const int32_t* start_pos;
+    const uint8_t* k_new;
+    const uint8_t* v_new;
+    uint32_t batch;
+    uint32_t n_new;
+    uint32_t hkv;
+    uint32_t head_dim;
+    uint32_t block_tokens;
+    uint32_t max_blocks;
+    uint32_t num_blocks;
+};
+
+// One work item = one group of 32 elements of one token-head row of K or V.
+template <int DT, int SRC>
+__global__ __launch_bounds__(256) void kv_append(AppendParams p) {
+    const uint32_t groups = p.head_dim / 32;
+    const uint64_t total = (uint64_t)p.batch * p.n_new * p.hkv * groups * 2;
+    for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
+         it += (uint64_t)gridDim.x * blockDim.x) {
+        const int which = (int)(it & 1);
+        uint64_t r = it >> 1;
+        const uint32_t g = (uint32_t)(r % groups);
+        r /= groups;
+        const uint32_t h = (uint32_t)(r % p.hkv);
+        r /= p.hkv;
+        const uint32_t i = (uint32_t)(r % p.n_new);
+        const uint32_t b = (uint32_t)(r / p.n_new);
+
+        const int32_t sp = p.start_pos[b];
+        if (sp < 0) continue;
+        const uint32_t pos = (uint32_t)sp + i;
+        const uint32_t lb = pos / p.block_tokens;
+        if (lb >= p.max_blocks) continue;
+        const int32_t phys = p.block_tables[(size_t)b * p.max_blocks + lb];
+        if (phys < 0 || (uint32_t)phys >= p.num_blocks) continue;
+        const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + pos % p.block_tokens;
+        const size_t src_el = (((size_t)b * p.n_new + i) * p.hkv + h) * p.head_dim + (size_t)g * 32;
+
+        float x[32];
+        const uint8_t* src = which ? p.v_new : p.k_new;
+        if constexpr (SRC == VSPEC_KV_F32) {
+            const float4* s4 = reinterpret_cast<const float4*>(src + src_el * 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float4 w = s4[j];
+                x[4 * j] = w.x; x[4 * j + 1] = w.y; x[4 * j + 2] = w.z; x[4 * j + 3] = w.w;
+            }
+        } else {
+            const uint4* s4 = reinterpret_cast<const uint4*>(src + src_el * 2);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) unpack_f16x8(s4[j], x + 8 * j);
+        }
+
+        uint8_t* dst = which ? p.v : p.k;
+        if constexpr (DT == VSPEC_KV_F32) {
+            float4* d4 = reinterpret_cast<float4*>(dst + (row * p.head_dim + (size_t)g * 32) * 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) d4[j] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+        } else if constexpr (DT == VSPEC_KV_F16) {
+            uint4* d4 = reinterpret_cast<uint4*>(dst + (row * p.head_dim + (size_t)g * 32) * 2);
+            if constexpr (SRC == VSPEC_KV_F16) {
+                // pure copy of the source bits
+                const uint4* s4 = reinterpret_cast<const uint4*>(src + src_el * 2);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) d4[j] = s4[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        w[k] = float_to_half_bits(x[8 * j + 2 * k]) |
+                               (float_to_half_bits(x[8 * j + 2 * k + 1]) << 16);
+                    }
+                    d4[j] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
+        } else {
+            // int4 codec: rep = 2nd-largest |x|, scale = rep/8 (1 if rep == 0),
+            // floored at 1e-6, rounded to fp16 (saturating), codes rint(x/scale) in [-8,7]
+            float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const float a = fabsf(x[e]);
+                if (a > a1) {
+                    a2 = a1;
+                    a1 = a;
+                } else if (a > a2) {
+                    a2 = a;
+                }
+            }
+            float scale = a2 > 0.f ? a2 / 8.0f : 1.0f;
+            if (scale < 1e-6f) scale = 1e-6f;
+            uint32_t s16 = float_to_half_bits(scale);
+            if ((s16 & 0x7fffu) >= 0x7c00u) s16 = 0x7bffu;
+            const float sc = half_bits_to_float(s16);
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const float rr = rintf(x[e] / sc);
+                const int code = rr > 7.0f ? 7 : (rr >= -8.0f ? (int)rr : -8);
+                w[e / 8] |= ((uint32_t)code & 0xfu) << (4 * (e % 8));
+            }
+            uint4* d4 = reinterpret_cast<uint4*>(dst + row * (p.head_dim / 2) + (size_t)g * 16);
+            *d4 = make_uint4(w[0], w[1], w[2], w[3]);
+            uint16_t* sd = which ? p.vs : p.ks;
+            sd[row * groups + g] = (uint16_t)s16;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// gather / compaction
+// ---------------------------------------------------------------------------
+struct GatherParams {
+    const uint8_t* k;
+    const uint8_t* v;
+    const uint16_t* ks;
+    const uint16_t* vs;
+    const int32_t* block_tables;
+    const int32_t* ctx_lens;
+    const int64_t* out_off;
+    uint8_t* ok;
+    uint8_t* ov;
+    uint16_t* oks;
+    uint16_t* ovs;
+    uint32_t hkv;
+    uint32_t head_dim;
+    uint32_t block_tokens;
+    uint32_t max_blocks;
+    uint32_t num_blocks;
+    uint32_t max_ctx;
+};
+
+// Raw gather: one thread per 16-byte chunk of a row (int4: 4-byte chunks plus
+// the row's scales).  Dequantising gather (OUTF32): one thread per 8 elements.
+template <int DT, int OUTF32>
+__global__ __launch_bounds__(256) void kv_gather(GatherParams p) {
+    const int b = blockIdx.y;
+    const int ctx = p.ctx_lens[b];
+    const uint32_t D = p.head_dim;
+    const uint32_t row_bytes = DT == VSPEC_KV_F32 ? D * 4 : (DT == VSPEC_KV_F16 ? D * 2 : D / 2);
+    const uint32_t cpr = OUTF32 ? D / 8 : (DT == VSPEC_KV_INT4 ? row_bytes / 4 : row_bytes / 16);
+    const uint64_t total = (uint64_t)p.max_ctx * p.hkv * cpr * 2;
+    for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
+         it += (uint64_t)gridDim.x * blockDim.x) {
+        const int which = (int)(it & 1);
+        uint64_t r = it >> 1;
+        const uint32_t c = (uint32_t)(r % cpr);
+        r /= cpr;
+        const uint32_t h = (uint32_t)(r % p.hkv);
+        const uint32_t t = (uint32_t)(r / p.hkv);
+        if ((int)t >= ctx) continue;
+        const uint32_t lb = t / p.block_tokens;
+        if (lb >= p.max_blocks) continue;
+        const int32_t phys = p.block_tables[(size_t)b * p.max_blocks + lb];
+        if (phys < 0 || (uint32_t)phys >= p.num_blocks) continue;
+        const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + t % p.block_tokens;
+        const size_t orow = ((size_t)p.out_off[b] + t) * p.hkv + h;
+        const uint8_t* src = which ? p.v : p.k;
+        uint8_t* dst = which ? p.ov : p.ok;
+        if constexpr (OUTF32) {
+            float x[8];
+            if constexpr (DT == VSPEC_KV_F32) {
+                const float4* s = reinterpret_cast<const float4*>(src + row * row_bytes) + 2 * c;
+                const float4 a = s[0], bb = s[1];
+                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+                x[4] = bb.x; x[5] = bb.y; x[6] = bb.z; x[7] = bb.w;
+            } else if constexpr (DT == VSPEC_KV_F16) {
+                unpack_f16x8(reinterpret_cast<const uint4*>(src + row * row_bytes)[c], x);
+            } else {
+                const uint32_t w = reinterpret_cast<const uint32_t*>(src + row * row_bytes)[c];
+                const uint16_t* sc = which ? p.vs : p.ks;
+                const float s = half_bits_to_float(sc[row * (D / 32) + c / 4]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[i] = nibble(w, i) * s;
+            }
+            float4* d = reinterpret_cast<float4*>(dst + orow * (size_t)D * 4) + 2 * c;
+            d[0] = make_float4(x[0], x[1], x[2], x[3]);
+            d[1] = make_float4(x[4], x[5], x[6], x[7]);
+        } else if constexpr (DT == VSPEC_KV_INT4) {
+            reinterpret_cast<uint32_t*>(dst + orow * row_bytes)[c] =
+                reinterpret_cast<const uint32_t*>(src + row * row_bytes)[c];
+            if (c < D / 32) {
+                const uint16_t* sc = which ? p.vs : p.ks;
+                uint16_t* od = which ? p.ovs : p.oks;
+                od[orow * (D / 32) + c] = sc[row * (D / 32) + c];
+            }
+        } else {
+            reinterpret_cast<uint4*>(dst + orow * row_bytes)[c] =
+                reinterpret_cast<const uint4*>(src + row * row_bytes)[c];
+        }
+    }
+}
+
+struct CompactParams {
+    uint8_t* k;
+    uint8_t* v;
+    uint16_t* ks;
+    uint16_t* vs;
+    const int32_t* src;
+    const int32_t* dst;
+    uint32_t n;
+    uint32_t num_blocks;
+    uint64_t block_bytes;    // data bytes per physical block (all heads), multiple of 16
+    uint64_t block_scales;   // scale entries per physical block (int4)
+};
+
+__global__ __launch_bounds__(256) void kv_compact(CompactParams p) {
+    const uint32_t i = blockIdx.y;
+    const int32_t s = p.src[i], d = p.dst[i];
+    if (s < 0 || d < 0 || (uint32_t)s >= p.num_blocks || (uint32_t)d >= p.num_blocks) return;
+    const uint64_t n16 = p.block_bytes / 16;
+    for (uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; j < 2 * n16;
+         j += (uint64_t)gridDim.x * blockDim.x) {
+        uint8_t* base = j < n16 ? p.k : p.v;
+        const uint64_t jj = j < n16 ? j : j - n16;
+        reinterpret_cast<uint4*>(base + (uint64_t)d * p.block_bytes)[jj] =
+            reinterpret_cast<const uint4*>(base + (uint64_t)s * p.block_bytes)[jj];
+    }
+    if (p.block_scales) {
+        for (uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; j < 2 * p.block_scales;
+             j += (uint64_t)gridDim.x * blockDim.x) {
+            uint16_t* base = j < p.block_scales ? p.ks : p.vs;
+            const uint64_t jj = j < p.block_scales ? j : j - p.block_scales;
+            base[(uint64_t)d * p.block_scales + jj] = base[(uint64_t)s * p.block_scales + jj];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host helpers
+// ---------------------------------------------------------------------------
+int g_num_cus = 0;
+
+int num_cus() {
+    if (g_num_cus > 0) return g_num_cus;
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+        prop.multiProcessorCount > 0) {
+        g_num_cus = prop.multiProcessorCount;
+    } else {
+        g_num_cus = 256;
+    }
+    return g_num_cus;
+}
+
+size_t row_bytes_of(int32_t dtype, uint32_t d) {
+    return dtype == VSPEC_KV_F32 ? (size_t)d * 4 : (dtype == VSPEC_KV_F16 ? (size_t)d * 2 : d / 2);
+}
+
+int check_kv(const VspecPagedKV* kv, const char* who) {
+    if (!kv) {
+        set_err("%s: null pool", who);
+        return 0;
+    }
+    if (kv->dtype < VSPEC_KV_F32 || kv->dtype > VSPEC_KV_INT4) {
+        set_err("%s: bad dtype %d", who, (int)kv->dtype);
+        return 0;
+    }
+    if (kv->num_blocks == 0 || kv->num_kv_heads == 0) {
+        set_err("%s: empty pool", who);
+        return 0;
+    }
+    if (kv->block_tokens == 0 || kv->block_tokens % kTile != 0) {
+        set_err("%s: block_tokens must be a positive multiple of %d", who, kTile);
+        return 0;
+    }
+    if (kv->head_dim != 64 && kv->head_dim != 128) {
+        set_err("%s: head_dim must be 64 or 128", who);
+        return 0;
+    }
+    if (!kv->k_data || !kv->v_data) {
+        set_err("%s: null pool data", who);
+        return 0;
+    }
+    if (kv->dtype == VSPEC_KV_INT4 && (!kv->k_scales || !kv->v_scales)) {
+        set_err("%s: int4 pool without scales", who);
+        return 0;
+    }
+    return 1;
+}
+
+// grow-only library workspace per device (used when the caller passes none)
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+Workspace g_ws[64];
+
+void* library_workspace(size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    Workspace& w = g_ws[dev];
+    if (w.bytes >= bytes) return w.ptr;
+    if (w.ptr) (void)hipFree(w.ptr);
+    w.ptr = nullptr;
+    w.bytes = 0;
+    if (hipMalloc(&w.ptr, bytes) != hipSuccess) {
+        w.ptr = nullptr;
+        return nullptr;
+    }
+    w.bytes = bytes;
+    return w.ptr;
+}
+
+struct DecodePlan {
+    uint32_t gw;
+    uint32_t gsplit;
+    uint32_t tiles_per_part;
+    uint32_t max_parts;
+    size_t ws_bytes;
+};
+
+int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
+    const uint32_t hkv = d->kv.num_kv_heads;
+    if (d->num_q_heads == 0 || d->num_q_heads % hkv != 0) {
+        set_err("paged_decode: num_q_heads must be a positive multiple of num_kv_heads");
+        return 0;
+    }
+    const uint32_t g = d->num_q_heads / hkv;
+    if (g <= 4) {
+        pl->gw = g;
+        pl->gsplit = 1;
+    } else if (g % 4 == 0) {
+        pl->gw = 4;
+        pl->gsplit = g / 4;
+    } else {
+        set_err("paged_decode: GQA group %u unsupported (need <= 4 or a multiple of 4)", g);
+        return 0;
+    }
+    const uint32_t max_tiles = (d->max_ctx_len + kTile - 1) / kTile;
+    uint32_t tpp;
+    if (d->partition_tokens) {
+        if (d->partition_tokens % kTile) {
+            set_err("paged_decode: partition_tokens must be a multiple of %d", kTile);
+            return 0;
+        }
+        tpp = d->partition_tokens / kTile;
+    } else {
+        // enough workgroups to fill the chip a few times over, partitions of >= 16 tiles
+        const uint64_t items = (uint64_t)d->batch * hkv * pl->gsplit;
+        const uint64_t target = 4ull * (uint64_t)num_cus();
+        uint64_t parts = items ? (target + items - 1) / items : 1;
+        if (parts < 1) parts = 1;
+        tpp = (uint32_t)((max_tiles + parts - 1) / parts);
+        if (tpp < 16) tpp = 16;
+        tpp = (tpp + kWaves - 1) / kWaves * kWaves;
+    }
+    if (tpp == 0) tpp = 1;
+    pl->tiles_per_part = tpp;
+    pl->max_parts = max_tiles ? (max_tiles + tpp - 1) / tpp : 1;
+    if (pl->max_parts == 0) pl->max_parts = 1;
+    pl->ws_bytes = pl->max_parts > 1
+                       ? (size_t)d->batch * d->num_q_heads * pl->max_parts * (2 + d->kv.head_dim) * sizeof(float)
+                       : 0;
+    return 1;
+}
+
+template <int DT, int D, int GW>
+void launch_partial(const DecodeParams& p, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((decode_partial<DT, D, GW>), grid, dim3(256), 0, s, p);
+}
+
+template <int DT, int D>
+int dispatch_gw(uint32_t gw, const DecodeParams& p, dim3 grid, hipStream_t s) {
+    switch (gw) {
+        case 1: launch_partial<DT, D, 1>(p, grid, s); return 1;
+        case 2: launch_partial<DT, D, 2>(p, grid, s); return 1;
+        case 3: launch_partial<DT, D, 3>(p, grid, s); return 1;
+        case 4: launch_partial<DT, D, 4>(p, grid, s); return 1;
+        default: return 0;
+    }
+}
+
+template <int DT>
+int dispatch_d(uint32_t d, uint32_t gw, const DecodeParams& p, dim3 grid, hipStream_t s) {
+    if (d == 64) return dispatch_gw<DT, 64>(gw, p, grid, s);
+    if (d == 128) return dispatch_gw<DT, 128>(gw, p, grid, s);
+    return 0;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* vspec_rocm_last_error(void) { return g_err; }
+
+int vspec_rocm_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int vspec_rocm_sync(void* stream) {
+    HIP_CHECK(hipStreamSynchronize((hipStream_t)stream), "sync");
+    return 1;
+}
+
+size_t vspec_rocm_kv_pool_bytes(int32_t dtype, uint32_t num_blocks, uint32_t block_tokens,
+                                uint32_t num_kv_heads, uint32_t head_dim) {
+    const size_t rows = (size_t)num_blocks * num_kv_heads * block_tokens;
+    size_t bytes = 2 * rows * row_bytes_of(dtype, head_dim);
+    if (dtype == VSPEC_KV_INT4) bytes += 2 * rows * (head_dim / 32) * sizeof(uint16_t);
+    return bytes;
+}
+
+int vspec_rocm_kv_pool_create(VspecPagedKV* kv, int32_t dtype, uint32_t num_blocks,
+                              uint32_t block_tokens, uint32_t num_kv_heads, uint32_t head_dim) {
+    if (!kv) {
+        set_err("kv_pool_create: null descriptor");
+        return 0;
+    }
+    memset(kv, 0, sizeof(*kv));
+    kv->dtype = dtype;
+    kv->num_blocks = num_blocks;
+    kv->block_tokens = block_tokens;
+    kv->num_kv_heads = num_kv_heads;
+    kv->head_dim = head_dim;
+    kv->k_data = kv->v_data = (void*)1;  // placeholders for validation
+    kv->k_scales = kv->v_scales = (uint16_t*)1;
+    if (!check_kv(kv, "kv_pool_create")) {
+        memset(kv, 0, sizeof(*kv));
+        return 0;
+    }
+    kv->k_data = kv->v_data = nullptr;
+    kv->k_scales = kv->v_scales = nullptr;
+    const size_t rows = (size_t)num_blocks * num_kv_heads * block_tokens;
+    const size_t data = rows * row_bytes_of(dtype, head_dim);
+    if (hipMalloc(&kv->k_data, data) != hipSuccess || hipMalloc(&kv->v_data, data) != hipSuccess) {
+        set_err("kv_pool_create: hipMalloc of %zu bytes failed", 2 * data);
+        vspec_rocm_kv_pool_destroy(kv);
+        return 0;
+    }
+    if (dtype == VSPEC_KV_INT4) {
+        const size_t sb = rows * (head_dim / 32) * sizeof(uint16_t);
+        if (hipMalloc((void**)&kv->k_scales, sb) != hipSuccess ||
+            hipMalloc((void**)&kv->v_scales, sb) != hipSuccess) {
+            set_err("kv_pool_create: hipMalloc of scales failed");
+            vspec_rocm_kv_pool_destroy(kv);
+            return 0;
+        }
+    }
+    return 1;
+}
+
+void vspec_rocm_kv_pool_destroy(VspecPagedKV* kv) {
+    if (!kv) return;
+    if (kv->k_data) (void)hipFree(kv->k_data);
+    if (kv->v_data) (void)hipFree(kv->v_data);
+    if (kv->k_scales) (void)hipFree(kv->k_scales);
+    if (kv->v_scales) (void)hipFree(kv->v_scales);
+    memset(kv, 0, sizeof(*kv));
+}
+
+int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                         uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                         const void* k_new, const void* v_new, int32_t src_dtype, void* stream) {
+    if (!check_kv(kv, "kv_append")) return 0;
+    if (src_dtype != VSPEC_KV_F32 && src_dtype != VSPEC_KV_F16) {
+        set_err("kv_append: src_dtype must be f32 or f16");
+        return 0;
+    }
+    if (batch == 0 || n_new == 0) return 1;
+    if (!block_tables || !start_pos || !k_new || !v_new || max_blocks_per_seq == 0) {
+        set_err("kv_append: null argument");
+        return 0;
+    }
+    AppendParams p;
+    p.k = (uint8_t*)kv->k_data;
+    p.v = (uint8_t*)kv->v_data;
+    p.ks = kv->k_scales;
+    p.vs = kv->v_scales;
+    p.block_tables = block_tables;
+    p.start_pos = start_pos;
+    p.k_new = (const uint8_t*)k_new;
+    p.v_new = (const uint8_t*)v_new;
+    p.batch = batch;
+    p.n_new = n_new;
+    p.hkv = kv->num_kv_heads;
+    p.head_dim = kv->head_dim;
+    p.block_tokens = kv->block_tokens;
+    p.max_blocks = max_blocks_per_seq;
+    p.num_blocks = kv->num_blocks;
+    const uint64_t items = (uint64_t)batch * n_new * kv->num_kv_heads * (kv->head_dim / 32) * 2;
+    uint64_t blocks = (items + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    const dim3 grid((unsigned)blocks);
+    hipStream_t s = (hipStream_t)stream;
+#define VSPEC_APPEND(DT, SRC) hipLaunchKernelGGL((kv_append<DT, SRC>), grid, dim3(256), 0, s, p)
+    if (src_dtype == VSPEC_KV_F32) {
+        if (kv->dtype == VSPEC_KV_F32) VSPEC_APPEND(VSPEC_KV_F32, VSPEC_KV_F32);
+        else if (kv->dtype == VSPEC_KV_F16) VSPEC_APPEND(VSPEC_KV_F16, VSPEC_KV_F32);
+        else VSPEC_APPEND(VSPEC_KV_INT4, VSPEC_KV_F32);
+    } else {
+        if (kv->dtype == VSPEC_KV_F32) VSPEC_APPEND(VSPEC_KV_F32, VSPEC_KV_F16);
+        else if (kv->dtype == VSPEC_KV_F16) VSPEC_APPEND(VSPEC_KV_F16, VSPEC_KV_F16);
+        else VSPEC_APPEND(VSPEC_KV_INT4, VSPEC_KV_F16);
+    }
+#undef VSPEC_APPEND
+    HIP_CHECK(hipGetLastError(), "kv_append launch");
+    return 1;
+}
+
+int vspec_rocm_kv_gather(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                         uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                         uint32_t max_ctx_len, const int64_t* out_token_offset, int32_t out_mode,
+                         void* out_k, void* out_v, uint16_t* out_k_scales,
+                         uint16_t* out_v_scales, void* stream) {
+    if (!check_kv(kv, "kv_gather")) return 0;
+    if (out_mode != VSPEC_GATHER_RAW && out_mode != VSPEC_GATHER_F32) {
+        set_err("kv_gather: bad out_mode");
+        return 0;
+    }
+    if (batch == 0 || max_ctx_len == 0) return 1;
+    if (!block_tables || !ctx_lens || !out_token_offset || !out_k || !out_v || max_blocks_per_seq == 0) {
+        set_err("kv_gather: null argument");
+        return 0;
+    }
+    if (out_mode == VSPEC_GATHER_RAW && kv->dtype == VSPEC_KV_INT4 && (!out_k_scales || !out_v_scales)) {
+        set_err("kv_gather: int4 raw gather needs scale outputs");
+        return 0;
+    }
+    GatherParams p;
+    p.k = (const uint8_t*)kv->k_data;
+    p.v = (const uint8_t*)kv->v_data;
+    p.ks = kv->k_scales;
+    p.vs = kv->v_scales;
+    p.block_tables = block_tables;
+    p.ctx_lens = ctx_lens;
+    p.out_off = out_token_offset;
+    p.ok = (uint8_t*)out_k;
+    p.ov = (uint8_t*)out_v;
+    p.oks = out_k_scales;
+    p.ovs = out_v_scales;
+    p.hkv = kv->num_kv_heads;
+    p.head_dim = kv->head_dim;
+    p.block_tokens = kv->block_tokens;
+    p.max_blocks = max_blocks_per_seq;
+    p.num_blocks = kv->num_blocks;
+    p.max_ctx = max_ctx_len;
+    const uint32_t D = kv->head_dim;
+    const size_t rb = row_bytes_of(kv->dtype, D);
+    const uint32_t cpr = out_mode == VSPEC_GATHER_F32 ? D / 8 : (kv->dtype == VSPEC_KV_INT4 ? rb / 4 : rb / 16);
+    const uint64_t items = (uint64_t)max_ctx_len * kv->num_kv_heads * cpr * 2;
+    uint64_t gx = (items + 255) / 256;
+    if (gx > 16384) gx = 16384;
+    const dim3 grid((unsigned)gx, batch);
+    hipStream_t s = (hipStream_t)stream;
+#define VSPEC_GATHER(DT, OF) hipLaunchKernelGGL((kv_gather<DT, OF>), grid, dim3(256), 0, s, p)
+    if (out_mode == VSPEC_GATHER_F32) {
+        if (kv->dtype == VSPEC_KV_F32) VSPEC_GATHER(VSPEC_KV_F32, 1);
+        else if (kv->dtype == VSPEC_KV_F16) VSPEC_GATHER(VSPEC_KV_F16, 1);
+        else VSPEC_GATHER(VSPEC_KV_INT4, 1);
+    } else {
+        if (kv->dtype == VSPEC_KV_F32) VSPEC_GATHER(VSPEC_KV_F32, 0);
+        else if (kv->dtype == VSPEC_KV_F16) VSPEC_GATHER(VSPEC_KV_F16, 0);
+        else VSPEC_GATHER(VSPEC_KV_INT4, 0);
+    }
+#undef VSPEC_GATHER
+    HIP_CHECK(hipGetLastError(), "kv_gather launch");
+    return 1;
+}
+
+int vspec_rocm_kv_compact(const VspecPagedKV* kv, uint32_t n, const int32_t* src_blocks,
+                          const int32_t* dst_blocks, void* stream) {
+    if (!check_kv(kv, "kv_compact")) return 0;
+    if (n == 0) return 1;
+    if (!src_blocks || !dst_blocks) {
+        set_err("kv_compact: null block list");
+        return 0;
+    }
+    CompactParams p;
+    p.k = (uint8_t*)kv->k_data;
+    p.v = (uint8_t*)kv->v_data;
+    p.ks = kv->k_scales;
+    p.vs = kv->v_scales;
+    p.src = src_blocks;
+    p.dst = dst_blocks;
+    p.n = n;
+    p.num_blocks = kv->num_blocks;
+    const uint64_t rows = (uint64_t)kv->num_kv_heads * kv->block_tokens;
+    p.block_bytes = rows * row_bytes_of(kv->dtype, kv->head_dim);
+    p.block_scales = kv->dtype == VSPEC_KV_INT4 ? rows * (kv->head_dim / 32) : 0;
+    uint64_t gx = (2 * (p.block_bytes / 16) + 255) / 256;
+    if (gx > 64) gx = 64;
+    if (gx == 0) gx = 1;
+    hipLaunchKernelGGL(kv_compact, dim3((unsigned)gx, n), dim3(256), 0, (hipStream_t)stream, p);
+    HIP_CHECK(hipGetLastError(), "kv_compact launch");
+    return 1;
+}
+
+size_t vspec_rocm_paged_decode_workspace_bytes(const VspecPagedAttnDesc* desc) {
+    DecodePlan pl;
+    if (!desc || !plan_decode(desc, &pl)) return 0;
+    return pl.ws_bytes;
+}
+
+int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
+    if (!desc) {
+        set_err("paged_decode: null descriptor");
+        return 0;
+    }
+    if (!check_kv(&desc->kv, "paged_decode")) return 0;
+    if (desc->batch == 0) return 1;
+    if (!desc->block_tables || !desc->ctx_lens || !desc->q || !desc->out || desc->max_blocks_per_seq == 0) {
+        set_err("paged_decode: null argument");
+        return 0;
+    }
+    if (desc->numerics != VSPEC_NUMERICS_PLAIN && desc->numerics != VSPEC_NUMERICS_3BIT) {
+        set_err("paged_decode: bad numerics mode");
+        return 0;
+    }
+    if ((uint64_t)desc->max_ctx_len > (uint64_t)desc->max_blocks_per_seq * desc->kv.block_tokens) {
+        set_err("paged_decode: max_ctx_len exceeds the block table");
+        return 0;
+    }
+    DecodePlan pl;
+    if (!plan_decode(desc, &pl)) return 0;
+    void* ws = nullptr;
+    if (pl.ws_bytes) {
+        if (desc->workspace) {
+            if (desc->workspace_bytes < pl.ws_bytes) {
+                set_err("paged_decode: workspace too small (%zu < %zu)", desc->workspace_bytes, pl.ws_bytes);
+                return 0;
+            }
+            ws = desc->workspace;
+        } else {
+            ws = library_workspace(pl.ws_bytes);
+            if (!ws) {
+                set_err("paged_decode: cannot allocate %zu workspace bytes", pl.ws_bytes);
+                return 0;
+            }
+        }
+    }
+    const uint32_t D = desc->kv.head_dim;
+    float scale = desc->scale > 0.f ? desc->scale : 1.0f / sqrtf((float)D);
+    const bool three = desc->numerics == VSPEC_NUMERICS_3BIT;
+    if (three) scale = fminf(fmaxf(scale, 1e-4f), 32.0f);
+
+    DecodeParams p;
+    p.k = (const uint8_t*)desc->kv.k_data;
+    p.v = (const uint8_t*)desc->kv.v_data;
+    p.ks = desc->kv.k_scales;
+    p.vs = desc->kv.v_scales;
+    p.block_tables = desc->block_tables;
+    p.ctx_lens = desc->ctx_lens;
+    p.q = desc->q;
+    p.out = desc->out;
+    p.part_ml = (float*)ws;
+    p.part_acc = ws ? (float*)ws + (size_t)desc->batch * desc->num_q_heads * pl.max_parts * 2 : nullptr;
+    p.hq = desc->num_q_heads;
+    p.hkv = desc->kv.num_kv_heads;
+    p.block_tokens = desc->kv.block_tokens;
+    p.max_blocks = desc->max_blocks_per_seq;
+    p.num_blocks = desc->kv.num_blocks;
+    p.tiles_per_part = pl.tiles_per_part;
+    p.max_parts = pl.max_parts;
+    p.gsplit = pl.gsplit;
+    p.qscale = scale * kLog2e;
+    p.alpha = desc->clamp_alpha > 0.f ? desc->clamp_alpha : 4.5f;
+    p.logit_clip = three ? 24.0f * kLog2e : INFINITY;
+    p.input_clip = three ? 16.0f : INFINITY;
+
+    hipStream_t s = (hipStream_t)desc->stream;
+    const dim3 grid(pl.max_parts, desc->kv.num_kv_heads * pl.gsplit, desc->batch);
+    int ok = 0;
+    switch (desc->kv.dtype) {
+        case VSPEC_KV_F32: ok = dispatch_d<VSPEC_KV_F32>(D, pl.gw, p, grid, s); break;
+        case VSPEC_KV_F16: ok = dispatch_d<VSPEC_KV_F16>(D, pl.gw, p, grid, s); break;
+        default: ok = dispatch_d<VSPEC_KV_INT4>(D, pl.gw, p, grid, s); break;
+    }
+    if (!ok) {
+        set_err("paged_decode: no kernel for head_dim %u, group %u", D, pl.gw);
+        return 0;
+    }
+    HIP_CHECK(hipGetLastError(), "decode_partial launch");
+    if (pl.max_parts > 1) {
+        const dim3 cg(desc->num_q_heads, desc->batch);
+        if (D == 64) hipLaunchKernelGGL(decode_combine<64>, cg, dim3(64), 0, s, p);
+        else hipLaunchKernelGGL(decode_combine<128>, cg, dim3(128), 0, s, p);
+        HIP_CHECK(hipGetLastError(), "decode_combine launch");
+    }
+    return 1;
+}
+
+}  // extern "C"
