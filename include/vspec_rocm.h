@@ -11,9 +11,11 @@
  *     (one stream per pool), as the reference's structs are unsynchronised.
  *
  * HBM layout (decision D6), element (block b, kv head h, slot s, dim d):
- *   f32 / f16 pools   data[((b*H + h)*P + s)*D + d]
- *   int4 pools        codes byte ((b*H + h)*P + s)*(D/2) + d/2, nibble d&1 (even = low);
- *                     scale  ((b*H + h)*P + s)*(D/32) + d/32, fp16 bits
+ *   K, and V of f32 pools  data[((b*H + h)*P + s)*D + d]          (token-major rows)
+ *   V of f16 pools         data[((b*H + h)*D + d)*P + s]          (d-major: the matrix-core
+ *                          operand of P.V needs consecutive tokens of one d per lane)
+ *   int4 pools (K and V)   codes byte ((b*H + h)*P + s)*(D/2) + d/2, nibble d&1 (even = low);
+ *                          scale  ((b*H + h)*P + s)*(D/32) + d/32, fp16 bits
  * so one (block, head) tile of P tokens is contiguous (4 KB at P=16, D=128, f16).
  *
  * int4 codec (decision D1): per (token, kv head) groups of 32 elements;

@@ -1,6 +1,6 @@
 /*
  * ref_shim.c -- harness linked with the reference's own hot-path sources
- * (compiled in place from the reference tree by oracle/ref.mk) into
+ * (compiled in place from the reference tree by oracle/Makefile) into
  * oracle/_ref/libvspec_ref.so.
  *
  * TEST INFRASTRUCTURE ONLY.  It gives Python (ctypes) opaque handles to the

@@ -606,11 +606,21 @@ static long vo_phys_block(const VoPagedKV* kv, const int32_t* block_tables, uint
     return (long)pb;
 }
 
+/* f16 V tiles are d-major: element (d, slot) of tile (b, h) at ((b*H + h)*D + d)*P + slot.
+ * Every other array is token-major (row index (b*H + h)*P + slot). */
+static int vo_v_dmajor(const VoPagedKV* kv, int is_v) { return is_v && kv->dtype == 1; }
+
 /* Write one token-head row (D elements) from fp32 values into the pool. */
-static void vo_store_row(const VoPagedKV* kv, void* data, uint16_t* scales, size_t row,
+static void vo_store_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
                          const float* src) {
-    const size_t D = kv->head_dim;
-    if (kv->dtype == 0) {
+    const size_t D = kv->head_dim, P = kv->block_tokens;
+    void* data = is_v ? kv->v_data : kv->k_data;
+    uint16_t* scales = is_v ? kv->v_scales : kv->k_scales;
+    const size_t row = vo_row_index(kv, b, h, slot);
+    if (vo_v_dmajor(kv, is_v)) {
+        uint16_t* t = (uint16_t*)data + (b * kv->num_kv_heads + h) * D * P + slot;
+        for (size_t d = 0; d < D; ++d) t[d * P] = vo_float_to_half(src[d]);
+    } else if (kv->dtype == 0) {
         memcpy((float*)data + row * D, src, D * sizeof(float));
     } else if (kv->dtype == 1) {
         vo_f32_to_f16(src, (uint16_t*)data + row * D, D);
@@ -620,16 +630,42 @@ static void vo_store_row(const VoPagedKV* kv, void* data, uint16_t* scales, size
 }
 
 /* Read one token-head row from the pool as fp32 (exact for all three formats). */
-static void vo_load_row(const VoPagedKV* kv, const void* data, const uint16_t* scales, size_t row,
+static void vo_load_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
                         float* dst) {
-    const size_t D = kv->head_dim;
-    if (kv->dtype == 0) {
+    const size_t D = kv->head_dim, P = kv->block_tokens;
+    const void* data = is_v ? kv->v_data : kv->k_data;
+    const uint16_t* scales = is_v ? kv->v_scales : kv->k_scales;
+    const size_t row = vo_row_index(kv, b, h, slot);
+    if (vo_v_dmajor(kv, is_v)) {
+        const uint16_t* t = (const uint16_t*)data + (b * kv->num_kv_heads + h) * D * P + slot;
+        for (size_t d = 0; d < D; ++d) dst[d] = vo_half_to_float(t[d * P]);
+    } else if (kv->dtype == 0) {
         memcpy(dst, (const float*)data + row * D, D * sizeof(float));
     } else if (kv->dtype == 1) {
         vo_f16_to_f32((const uint16_t*)data + row * D, dst, D);
     } else {
         vo_int4_dequantize_head((const uint8_t*)data + row * (D / 2u), scales + row * (D / 32u), D,
                                 dst);
+    }
+}
+
+/* Raw (pool-format) copy of one token-head row into a token-major output row. */
+static void vo_copy_row_raw(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
+                            void* out_row, uint16_t* out_scales) {
+    const size_t D = kv->head_dim, P = kv->block_tokens, G = D / 32u;
+    const void* data = is_v ? kv->v_data : kv->k_data;
+    const uint16_t* scales = is_v ? kv->v_scales : kv->k_scales;
+    const size_t row = vo_row_index(kv, b, h, slot);
+    if (vo_v_dmajor(kv, is_v)) {
+        const uint16_t* t = (const uint16_t*)data + (b * kv->num_kv_heads + h) * D * P + slot;
+        for (size_t d = 0; d < D; ++d) ((uint16_t*)out_row)[d] = t[d * P];
+    } else if (kv->dtype == 0) {
+        memcpy(out_row, (const float*)data + row * D, D * 4u);
+    } else if (kv->dtype == 1) {
+        memcpy(out_row, (const uint16_t*)data + row * D, D * 2u);
+    } else {
+        memcpy(out_row, (const uint8_t*)data + row * (D / 2u), D / 2u);
+        memcpy(out_scales, scales + row * G, G * 2u);
     }
 }
 
@@ -661,9 +697,8 @@ int vo_paged_append(const VoPagedKV* kv, uint32_t batch, const int32_t* block_ta
                     vo_f16_to_f32((const uint16_t*)k_new + src_off, kr, D);
                     vo_f16_to_f32((const uint16_t*)v_new + src_off, vr, D);
                 }
-                const size_t row = vo_row_index(kv, (size_t)pb, h, slot);
-                vo_store_row(kv, kv->k_data, kv->k_scales, row, kr);
-                vo_store_row(kv, kv->v_data, kv->v_scales, row, vr);
+                vo_store_row(kv, 0, (size_t)pb, h, slot, kr);
+                vo_store_row(kv, 1, (size_t)pb, h, slot, vr);
             }
         }
     }
@@ -691,22 +726,16 @@ int vo_paged_gather(const VoPagedKV* kv, uint32_t batch, const int32_t* block_ta
             const size_t slot = t % kv->block_tokens;
             const size_t ot = (size_t)out_token_offset[b] + t;
             for (size_t h = 0; h < H; ++h) {
-                const size_t row = vo_row_index(kv, (size_t)pb, h, slot);
                 const size_t orow = ot * H + h;
                 if (out_mode == 1) {
-                    vo_load_row(kv, kv->k_data, kv->k_scales, row, (float*)out_k + orow * D);
-                    vo_load_row(kv, kv->v_data, kv->v_scales, row, (float*)out_v + orow * D);
-                } else if (kv->dtype == 0) {
-                    memcpy((float*)out_k + orow * D, (const float*)kv->k_data + row * D, D * 4u);
-                    memcpy((float*)out_v + orow * D, (const float*)kv->v_data + row * D, D * 4u);
-                } else if (kv->dtype == 1) {
-                    memcpy((uint16_t*)out_k + orow * D, (const uint16_t*)kv->k_data + row * D, D * 2u);
-                    memcpy((uint16_t*)out_v + orow * D, (const uint16_t*)kv->v_data + row * D, D * 2u);
+                    vo_load_row(kv, 0, (size_t)pb, h, slot, (float*)out_k + orow * D);
+                    vo_load_row(kv, 1, (size_t)pb, h, slot, (float*)out_v + orow * D);
                 } else {
-                    memcpy((uint8_t*)out_k + orow * (D / 2u), (const uint8_t*)kv->k_data + row * (D / 2u), D / 2u);
-                    memcpy((uint8_t*)out_v + orow * (D / 2u), (const uint8_t*)kv->v_data + row * (D / 2u), D / 2u);
-                    memcpy(out_k_scales + orow * G, kv->k_scales + row * G, G * 2u);
-                    memcpy(out_v_scales + orow * G, kv->v_scales + row * G, G * 2u);
+                    const size_t rb = kv->dtype == 0 ? D * 4u : (kv->dtype == 1 ? D * 2u : D / 2u);
+                    vo_copy_row_raw(kv, 0, (size_t)pb, h, slot, (uint8_t*)out_k + orow * rb,
+                                    out_k_scales ? out_k_scales + orow * G : NULL);
+                    vo_copy_row_raw(kv, 1, (size_t)pb, h, slot, (uint8_t*)out_v + orow * rb,
+                                    out_v_scales ? out_v_scales + orow * G : NULL);
                 }
             }
         }
@@ -767,9 +796,8 @@ int vo_paged_decode_attention(int mode, size_t dot_block, const VoPagedKV* kv, u
             for (size_t t = 0; t < T; ++t) {
                 const long pb = vo_phys_block(kv, block_tables, max_blocks_per_seq, b, t);
                 if (pb < 0) { ok = 0; break; }
-                const size_t row = vo_row_index(kv, (size_t)pb, hk, t % kv->block_tokens);
-                vo_load_row(kv, kv->k_data, kv->k_scales, row, kh + t * D);
-                vo_load_row(kv, kv->v_data, kv->v_scales, row, vh + t * D);
+                vo_load_row(kv, 0, (size_t)pb, hk, t % kv->block_tokens, kh + t * D);
+                vo_load_row(kv, 1, (size_t)pb, hk, t % kv->block_tokens, vh + t * D);
             }
             for (size_t g = 0; g < group && ok; ++g) {
                 const size_t hq = hk * group + g;

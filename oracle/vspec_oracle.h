@@ -9,8 +9,8 @@
  * the reference repository root).  The restatement is written from scratch in
  * plain C11 + libm and follows the reference's operation order so that it is
  * bit-identical to the reference C path where the reference defines the
- * behaviour (pinned by tests/test_oracle_vs_ref.py against oracle/_ref, the
- * reference's own sources compiled by oracle/ref.mk).
+ * behaviour (pinned by tests/test_oracle_pin.py against oracle/_ref, the
+ * reference's own sources compiled by oracle/Makefile).
  *
  * Formats the reference does not define (fp16 KV, int4 KV) are defined here
  * and in the product header include/vspec_rocm.h identically:
@@ -91,6 +91,7 @@ void vo_attention_ref_single_query(int mode, size_t dot_block, const float* quer
  * dtype: 0 = f32, 1 = f16, 2 = int4.
  * Element (block b, kv-head h, slot s, dim d):
  *   f32/f16 data index  ((b*H + h)*P + s)*D + d           (k_data / v_data)
+ *   except f16 V        ((b*H + h)*D + d)*P + s           (d-major tiles)
  *   int4 code byte      ((b*H + h)*P + s)*(D/2) + d/2     (nibble d&1)
  *   int4 scale index    ((b*H + h)*P + s)*(D/32) + d/32   (k_scales / v_scales, fp16 bits)
  */

@@ -85,10 +85,13 @@ def assert_pools_equal(host: HostPool, pool):
         if w is None:
             assert g is None
             continue
-        g = np.ascontiguousarray(g).view(np.uint8)
-        w = np.ascontiguousarray(w).view(np.uint8)
-        bad = np.flatnonzero(g != w)
-        assert bad.size == 0, f"{name}: {bad.size} bytes differ, first at {bad[:8]}"
+        ge = np.ascontiguousarray(g).reshape(-1)
+        we = np.ascontiguousarray(w).reshape(-1)
+        bad = np.flatnonzero(ge.view(np.uint8) != we.view(np.uint8))
+        if bad.size:
+            el = np.unique(bad // ge.itemsize)[:6]
+            detail = ", ".join(f"[{i}] gpu={ge[i]!r} oracle={we[i]!r}" for i in el)
+            raise AssertionError(f"{name}: {bad.size} bytes differ; elements {detail}")
 
 
 def build_both(oracle, case, dev, prefix_split=True):

@@ -43,98 +43,10 @@ extern "C" void vspec_rocm_set_error_(const char* msg) { set_err("%s", msg ? msg
         }                                                                  \
     } while (0)
 
-// ---------------------------------------------------------------------------
-// device helpers
-// ---------------------------------------------------------------------------
+#include "kv_common.h"
+
 namespace {
-
-constexpr int kTile = 16;   // tokens per attention tile
-constexpr int kWaves = 4;   // waves per attention workgroup
-constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
-}
-
-__device__ __forceinline__ uint32_t float_to_half_bits(float x) {
-    // v_cvt_f16_f32 under the default round-to-nearest-even mode
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x)));
-}
-
-__device__ __forceinline__ void unpack_f16x8(const uint4 w, float* out) {
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        out[2 * i] = half_bits_to_float(ws[i] & 0xffffu);
-        out[2 * i + 1] = half_bits_to_float(ws[i] >> 16);
-    }
-}
-
-// signed nibble i (0..7) of a 32-bit word, even element in the low nibble
-__device__ __forceinline__ float nibble(uint32_t w, int i) {
-    return static_cast<float>(static_cast<int32_t>(w << (28 - 4 * i)) >> 28);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
-}
-
-// DPP controls
-constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
-constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
-constexpr int kRowHalfMirror = 0x141;
-constexpr int kRowMirror = 0x140;
-
-// Sum over aligned groups of N lanes (N = 4, 8, 16); every lane gets the total.
-template <int N>
-__device__ __forceinline__ float group_sum(float x) {
-    static_assert(N == 4 || N == 8 || N == 16, "group size");
-    x += dpp<kQuadXor1>(x);
-    x += dpp<kQuadXor2>(x);
-    if constexpr (N >= 8) x += dpp<kRowHalfMirror>(x);
-    if constexpr (N >= 16) x += dpp<kRowMirror>(x);
-    return x;
-}
-
-// Max over the 64/N groups of a wave when x is uniform inside each aligned group of N.
-template <int N>
-__device__ __forceinline__ float max_across_groups(float x) {
-    if constexpr (N <= 4) x = fmaxf(x, dpp<kRowHalfMirror>(x));
-    if constexpr (N <= 8) x = fmaxf(x, dpp<kRowMirror>(x));
-    x = fmaxf(x, __shfl_xor(x, 16));
-    x = fmaxf(x, __shfl_xor(x, 32));
-    return x;
-}
-
-// ---------------------------------------------------------------------------
-// decode attention
-// ---------------------------------------------------------------------------
-struct DecodeParams {
-    const uint8_t* k;
-    const uint8_t* v;
-    const uint16_t* ks;
-    const uint16_t* vs;
-    const int32_t* block_tables;
-    const int32_t* ctx_lens;
-    const float* q;
-    float* out;
-    float* part_ml;    // [B][Hq][max_parts][2] (max in log2 units, sum)
-    float* part_acc;   // [B][Hq][max_parts][D]
-    uint32_t hq;
-    uint32_t hkv;
-    uint32_t block_tokens;
-    uint32_t max_blocks;
-    uint32_t num_blocks;
-    uint32_t tiles_per_part;
-    uint32_t max_parts;
-    uint32_t gsplit;   // work items per kv head (Hq/Hkv/GW)
-    float qscale;      // softmax scale * log2(e)
-    float alpha;       // std-clamp alpha
-    float logit_clip;  // +-24*log2(e) in 3-bit mode, +inf otherwise
-    float input_clip;  // 16 in 3-bit mode, +inf otherwise
-};
+using namespace vkv;
 
 // Per-dtype geometry of one row (one token of one kv head).
 template <int DT, int D>
@@ -518,6 +430,19 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) d4[j] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
         } else if constexpr (DT == VSPEC_KV_F16) {
+            if (which) {
+                // V tiles are d-major: element (d, slot) at tile + d*P + slot
+                const size_t tile = ((size_t)phys * p.hkv + h) * p.head_dim * p.block_tokens;
+                uint16_t* vt = reinterpret_cast<uint16_t*>(dst) + tile + pos % p.block_tokens;
+                const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src + src_el * 2);
+#pragma unroll
+                for (int e = 0; e < 32; ++e) {
+                    const size_t d = (size_t)g * 32 + e;
+                    vt[d * p.block_tokens] =
+                        SRC == VSPEC_KV_F16 ? s16[e] : (uint16_t)float_to_half_bits(x[e]);
+                }
+                continue;
+            }
             uint4* d4 = reinterpret_cast<uint4*>(dst + (row * p.head_dim + (size_t)g * 32) * 2);
             if constexpr (SRC == VSPEC_KV_F16) {
                 // pure copy of the source bits
@@ -620,6 +545,27 @@ __global__ __launch_bounds__(256) void kv_gather(GatherParams p) {
         const size_t orow = ((size_t)p.out_off[b] + t) * p.hkv + h;
         const uint8_t* src = which ? p.v : p.k;
         uint8_t* dst = which ? p.ov : p.ok;
+        if (DT == VSPEC_KV_F16 && which) {
+            // d-major V tile: 8 elements of column `slot`, stride P
+            const uint16_t* vt = reinterpret_cast<const uint16_t*>(src) +
+                                 ((size_t)phys * p.hkv + h) * D * p.block_tokens + t % p.block_tokens;
+            const uint32_t d0 = 8 * c;
+            uint16_t e16[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) e16[i] = vt[(size_t)(d0 + i) * p.block_tokens];
+            if (OUTF32) {
+                float4* d = reinterpret_cast<float4*>(dst + orow * (size_t)D * 4) + 2 * c;
+                d[0] = make_float4(half_bits_to_float(e16[0]), half_bits_to_float(e16[1]),
+                                   half_bits_to_float(e16[2]), half_bits_to_float(e16[3]));
+                d[1] = make_float4(half_bits_to_float(e16[4]), half_bits_to_float(e16[5]),
+                                   half_bits_to_float(e16[6]), half_bits_to_float(e16[7]));
+            } else {
+                reinterpret_cast<uint4*>(dst + orow * row_bytes)[c] =
+                    make_uint4(e16[0] | ((uint32_t)e16[1] << 16), e16[2] | ((uint32_t)e16[3] << 16),
+                               e16[4] | ((uint32_t)e16[5] << 16), e16[6] | ((uint32_t)e16[7] << 16));
+            }
+            continue;
+        }
         if constexpr (OUTF32) {
             float x[8];
             if constexpr (DT == VSPEC_KV_F32) {
@@ -800,9 +746,11 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
         }
         tpp = d->partition_tokens / kTile;
     } else {
-        // enough workgroups to fill the chip a few times over, partitions of >= 16 tiles
+        // split each (sequence, kv head) only as far as needed to occupy every resident
+        // workgroup slot once (two 4-wave workgroups per CU at the kernels' register
+        // use); extra partitions only add combine traffic and per-workgroup setup
         const uint64_t items = (uint64_t)d->batch * hkv * pl->gsplit;
-        const uint64_t target = 4ull * (uint64_t)num_cus();
+        const uint64_t target = 2ull * (uint64_t)num_cus();
         uint64_t parts = items ? (target + items - 1) / items : 1;
         if (parts < 1) parts = 1;
         tpp = (uint32_t)((max_tiles + parts - 1) / parts);
@@ -1132,7 +1080,7 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
     int ok = 0;
     switch (desc->kv.dtype) {
         case VSPEC_KV_F32: ok = dispatch_d<VSPEC_KV_F32>(D, pl.gw, p, grid, s); break;
-        case VSPEC_KV_F16: ok = dispatch_d<VSPEC_KV_F16>(D, pl.gw, p, grid, s); break;
+        case VSPEC_KV_F16: ok = launch_decode_mfma_f16(p, D, pl.gw, grid, s); break;
         default: ok = dispatch_d<VSPEC_KV_INT4>(D, pl.gw, p, grid, s); break;
     }
     if (!ok) {
