@@ -232,11 +232,16 @@ def main():
                            "p10_ms": attn_ms[len(attn_ms) // 10], "p90_ms": attn_ms[(9 * len(attn_ms)) // 10]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": traffic,
-                     "kernel": "decode_partial (+decode_combine when split-K partitions > 1)",
+                     "kernel": ("decode_mfma_f16" if wl["dtype"] == "f16" else "decode_partial")
+                               + (" + decode_combine" if ws_bytes else ""),
                      "algorithmic_bytes_per_launch": alg},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
+        # the parity spot check compares against pool 0 (the timed loop rotates pools)
+        if not L.vspec_rocm_paged_decode_attention(C.byref(descs[0])):
+            raise vr.VspecRocmError(vr.last_error())
+        torch.cuda.synchronize()
         result["cpu_baseline"] = cpu_baseline(args, wl, pools[0], tables_l[0], ctx, q, out, mode)
     print(json.dumps(result), flush=True)
 

@@ -35,17 +35,22 @@ struct Frags {
     uint2 v[D / 16];  // V^T row d = 16j + n, slots 4g .. 4g+3 of the tile
 };
 
-template <int D, int GW>
+// PB: block_tokens known at compile time (16), or 0 for any multiple of 16
+template <int D, int GW, int PB>
 __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     constexpr int NQK = D / 32;  // QK MFMAs per tile (each on 32 d)
     constexpr int NDT = D / 16;  // PV d-tiles
     __shared__ float qs[GW][D];
+    // QK B operands per lane (hi, lo for each 32-wide d chunk), read back every tile
+    __shared__ uint4 qb_lds[NQK][2][64];
     __shared__ float comb[kWaves][GW][D + 2];
     __shared__ float patch_val[kWaves][kTile][4];
     __shared__ int patch_flag[kWaves][kTile];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave index as a scalar: tile loop control and block-table reads stay on the
+    // scalar unit (s_load), so they never wait behind the vector K/V loads
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4;   // row group
     const int n = lane & 15;   // column / token within the tile
     const int part = blockIdx.x;
@@ -86,23 +91,28 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     __syncthreads();
 
     // B operands of the QK MFMAs: column n < GW holds head n, split hi + lo
-    h8_t qhi[NQK], qlo[NQK];
+    if (wave == 0) {
 #pragma unroll
-    for (int i = 0; i < NQK; ++i) {
+        for (int i = 0; i < NQK; ++i) {
+            h8_t hi8, lo8;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float qv = n < GW ? qs[n < GW ? n : 0][32 * i + 8 * g + j] : 0.f;
-            const _Float16 hi = (_Float16)qv;
-            qhi[i][j] = hi;
-            qlo[i][j] = (_Float16)(qv - (float)hi);
+            for (int j = 0; j < 8; ++j) {
+                const float qv = n < GW ? qs[n < GW ? n : 0][32 * i + 8 * g + j] : 0.f;
+                const _Float16 hi = (_Float16)qv;
+                hi8[j] = hi;
+                lo8[j] = (_Float16)(qv - (float)hi);
+            }
+            qb_lds[i][0][lane] = __builtin_bit_cast(uint4, hi8);
+            qb_lds[i][1][lane] = __builtin_bit_cast(uint4, lo8);
         }
     }
+    __syncthreads();
 
-    const int tiles_per_block = (int)p.block_tokens / kTile;
+    const int P = PB ? PB : (int)p.block_tokens;
+    const int tiles_per_block = P / kTile;
     const int32_t* table = p.block_tables + (size_t)b * p.max_blocks;
     const _Float16* kbase = reinterpret_cast<const _Float16*>(p.k);
     const _Float16* vbase = reinterpret_cast<const _Float16*>(p.v);
-    const int P = (int)p.block_tokens;
 
     auto load = [&](int tile, Frags<D>& f) -> bool {
         const int phys = table[tile / tiles_per_block];
@@ -125,163 +135,164 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     float l_run = 0.f;        // running sum of p for head n over this lane's tokens
     const h2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-    Frags<D> cur;
-    int tile = tile_begin + wave;
-    bool ok_cur = tile < tile_end ? load(tile, cur) : false;
-    while (tile < tile_end) {
-        const int next = tile + kWaves;
-        Frags<D> nxt;
-        bool ok_next = false;
-        if (next < tile_end) ok_next = load(next, nxt);
+    // one 16-token tile: clamp screen, scores, online softmax, P.V
+    auto process = [&](Frags<D>& f, const int tile) {
+        const int tok0 = tile * kTile;
+        const int nvalid = min(kTile, ctx - tok0);
 
-        if (ok_cur) {
-            const int tok0 = tile * kTile;
-            const int nvalid = min(kTile, ctx - tok0);
-
-            // ---- clamp screen for key n (this lane holds 8*NQK of its elements) ----
-            float s1 = 0.f, s2 = 0.f;
-            h2_t mx2 = {(_Float16)0.f, (_Float16)0.f};
+        // ---- clamp screen for key n (this lane holds 8*NQK of its elements) ----
+        float s1 = 0.f, s2 = 0.f;
+        h2_t mx2 = {(_Float16)0.f, (_Float16)0.f};
 #pragma unroll
-            for (int i = 0; i < NQK; ++i) {
-                const uint32_t w4[4] = {cur.k[i].x, cur.k[i].y, cur.k[i].z, cur.k[i].w};
+        for (int i = 0; i < NQK; ++i) {
+            const uint32_t w4[4] = {f.k[i].x, f.k[i].y, f.k[i].z, f.k[i].w};
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const h2_t kv2 = as_h2(w4[c]);
-                    s1 = __builtin_amdgcn_fdot2(kv2, ones, s1, false);
-                    s2 = __builtin_amdgcn_fdot2(kv2, kv2, s2, false);
-                    mx2 = __builtin_elementwise_max(mx2, __builtin_elementwise_abs(kv2));
-                }
-            }
-            float mx = fmaxf((float)mx2[0], (float)mx2[1]);
-            s1 += __shfl_xor(s1, 16);
-            s1 += __shfl_xor(s1, 32);
-            s2 += __shfl_xor(s2, 16);
-            s2 += __shfl_xor(s2, 32);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mean = s1 * (1.0f / D);
-            const float ex2 = s2 * (1.0f / D);
-            const float var1 = ex2 - mean * mean;
-            const float th1 = fminf(fmaxf(1e-6f, p.alpha * sqrtf(fmaxf(var1, 0.f))), p.input_clip);
-            // a margin of 2^-10 covers the one-pass variance error; ill-conditioned rows
-            // (variance tiny against the mean square) always take the exact path
-            const bool flag = (n < nvalid) && (mx > th1 * (1.0f - 0.0009765625f) || var1 <= ex2 * 0.0009765625f);
-
-            // ---- scores: S^T = K Q'^T (hi and lo accumulate into one column) ----
-            f4_t sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < NQK; ++i) {
-                sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(cur.k[i]), qhi[i], sc, 0, 0, 0);
-                sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(cur.k[i]), qlo[i], sc, 0, 0, 0);
-            }
-
-            // ---- exact scores for keys the clamp may change ----
-            if (__builtin_amdgcn_ballot_w64(flag) != 0) {
-                float part[GW];
-                float x[8 * NQK];
-#pragma unroll
-                for (int i = 0; i < NQK; ++i) {
-                    const uint32_t w4[4] = {cur.k[i].x, cur.k[i].y, cur.k[i].z, cur.k[i].w};
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        x[8 * i + 2 * c] = half_bits_to_float(w4[c] & 0xffffu);
-                        x[8 * i + 2 * c + 1] = half_bits_to_float(w4[c] >> 16);
-                    }
-                }
-                float v2 = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8 * NQK; ++e) v2 = fmaf(x[e] - mean, x[e] - mean, v2);
-                v2 += __shfl_xor(v2, 16);
-                v2 += __shfl_xor(v2, 32);
-                const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v2 * (1.0f / D))), p.input_clip);
-#pragma unroll
-                for (int h = 0; h < GW; ++h) {
-                    float a = 0.f;
-#pragma unroll
-                    for (int i = 0; i < NQK; ++i) {
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            a = fmaf(qs[h][32 * i + 8 * g + j], fminf(fmaxf(x[8 * i + j], -th), th), a);
-                        }
-                    }
-                    a += __shfl_xor(a, 16);
-                    a += __shfl_xor(a, 32);
-                    part[h] = a;
-                }
-                if (g == 0) {
-                    patch_flag[wave][n] = flag ? 1 : 0;
-#pragma unroll
-                    for (int h = 0; h < GW; ++h) patch_val[wave][n][h] = part[h];
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                if (n < GW) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int t = 4 * g + r;
-                        if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n];
-                    }
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-            }
-
-            // ---- online softmax for head n over tokens 4g..4g+3 ----
-            float s[4];
-            float mt = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = fminf(fmaxf(sc[r], -p.logit_clip), p.logit_clip);
-                s[r] = (n < GW && 4 * g + r < nvalid) ? v : -INFINITY;
-                mt = fmaxf(mt, s[r]);
-            }
-            mt = fmaxf(mt, __shfl_xor(mt, 16));
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const bool need = mt > m_run + 8.0f;
-            if (__builtin_amdgcn_ballot_w64(need) != 0) {
-                const float f = need ? exp2f(m_run - mt) : 1.0f;
-                m_run = need ? mt : m_run;
-                l_run *= f;
-#pragma unroll
-                for (int j = 0; j < NDT; ++j) acc[j] *= f;
-            }
-            float pr[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                pr[r] = s[r] == -INFINITY ? 0.f : exp2f(s[r] - m_run);  // masked / unused -> 0
-                l_run += pr[r];
-            }
-            h4_t phi, plo;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const _Float16 hi = (_Float16)pr[r];
-                phi[r] = hi;
-                plo[r] = (_Float16)(pr[r] - (float)hi);
-            }
-
-            // ---- O^T += V^T P^T ----
-            if (nvalid < kTile) {
-                // slots past the context may hold any bits (NaN): zero them
-#pragma unroll
-                for (int j = 0; j < NDT; ++j) {
-                    h4_t vv = as_h4(cur.v[j]);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (4 * g + r >= nvalid) vv[r] = (_Float16)0.f;
-                    }
-                    cur.v[j] = __builtin_bit_cast(uint2, vv);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < NDT; ++j) {
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(cur.v[j]), phi, acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(cur.v[j]), plo, acc[j], 0, 0, 0);
+            for (int c = 0; c < 4; ++c) {
+                const h2_t kv2 = as_h2(w4[c]);
+                s1 = __builtin_amdgcn_fdot2(kv2, ones, s1, false);
+                s2 = __builtin_amdgcn_fdot2(kv2, kv2, s2, false);
+                mx2 = __builtin_elementwise_max(mx2, __builtin_elementwise_abs(kv2));
             }
         }
-        cur = nxt;
-        ok_cur = ok_next;
-        tile = next;
+        float mx = fmaxf((float)mx2[0], (float)mx2[1]);
+        s1 += __shfl_xor(s1, 16);
+        s1 += __shfl_xor(s1, 32);
+        s2 += __shfl_xor(s2, 16);
+        s2 += __shfl_xor(s2, 32);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mean = s1 * (1.0f / D);
+        const float ex2 = s2 * (1.0f / D);
+        const float var1 = ex2 - mean * mean;
+        const float th1 = fminf(fmaxf(1e-6f, p.alpha * sqrtf(fmaxf(var1, 0.f))), p.input_clip);
+        // a margin of 2^-10 covers the one-pass variance error; ill-conditioned rows
+        // (variance tiny against the mean square) always take the exact path
+        const bool flag = (n < nvalid) && (mx > th1 * (1.0f - 0.0009765625f) || var1 <= ex2 * 0.0009765625f);
+
+        // ---- scores: S^T = K Q'^T (hi and lo accumulate into one column) ----
+        f4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NQK; ++i) {
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[i][0][lane]), sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[i][1][lane]), sc, 0, 0, 0);
+        }
+
+        // ---- exact scores for keys the clamp may change ----
+        if (__builtin_amdgcn_ballot_w64(flag) != 0) {
+            float part[GW];
+            float v2 = 0.f;
+#pragma unroll
+            for (int i = 0; i < NQK; ++i) {
+                const uint32_t w4[4] = {f.k[i].x, f.k[i].y, f.k[i].z, f.k[i].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = half_bits_to_float((w4[e / 2] >> (16 * (e % 2))) & 0xffffu);
+                    v2 = fmaf(x - mean, x - mean, v2);
+                }
+            }
+            v2 += __shfl_xor(v2, 16);
+            v2 += __shfl_xor(v2, 32);
+            const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v2 * (1.0f / D))), p.input_clip);
+#pragma unroll
+            for (int h = 0; h < GW; ++h) {
+                float a = 0.f;
+#pragma unroll
+                for (int i = 0; i < NQK; ++i) {
+                    const uint32_t w4[4] = {f.k[i].x, f.k[i].y, f.k[i].z, f.k[i].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float x = half_bits_to_float((w4[e / 2] >> (16 * (e % 2))) & 0xffffu);
+                        a = fmaf(qs[h][32 * i + 8 * g + e], fminf(fmaxf(x, -th), th), a);
+                    }
+                }
+                a += __shfl_xor(a, 16);
+                a += __shfl_xor(a, 32);
+                part[h] = a;
+            }
+            if (g == 0) {
+                patch_flag[wave][n] = flag ? 1 : 0;
+#pragma unroll
+                for (int h = 0; h < GW; ++h) patch_val[wave][n][h] = part[h];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (n < GW) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 4 * g + r;
+                    if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n];
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+
+        // ---- online softmax for head n over tokens 4g..4g+3 ----
+        float s[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float v = fminf(fmaxf(sc[r], -p.logit_clip), p.logit_clip);
+            s[r] = (n < GW && 4 * g + r < nvalid) ? v : -INFINITY;
+            mt = fmaxf(mt, s[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const bool need = mt > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(need) != 0) {
+            const float f = need ? exp2f(m_run - mt) : 1.0f;
+            m_run = need ? mt : m_run;
+            l_run *= f;
+#pragma unroll
+            for (int j = 0; j < NDT; ++j) acc[j] *= f;
+        }
+        float pr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pr[r] = s[r] == -INFINITY ? 0.f : exp2f(s[r] - m_run);  // masked / unused -> 0
+            l_run += pr[r];
+        }
+        h4_t phi, plo;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const _Float16 hi = (_Float16)pr[r];
+            phi[r] = hi;
+            plo[r] = (_Float16)(pr[r] - (float)hi);
+        }
+
+        // ---- O^T += V^T P^T ----
+        if (nvalid < kTile) {
+            // slots past the context may hold any bits (NaN): zero them
+#pragma unroll
+            for (int j = 0; j < NDT; ++j) {
+                h4_t vv = as_h4(f.v[j]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (4 * g + r >= nvalid) vv[r] = (_Float16)0.f;
+                }
+                f.v[j] = __builtin_bit_cast(uint2, vv);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NDT; ++j) {
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(f.v[j]), phi, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(f.v[j]), plo, acc[j], 0, 0, 0);
+        }
+    };
+
+    // two tiles in flight per wave: buffers A and B alternate, so a tile's loads are
+    // issued two tiles before it is processed and no registers are copied
+    Frags<D> fa, fb;
+    int tile = tile_begin + wave;
+    bool oka = tile < tile_end ? load(tile, fa) : false;
+    bool okb = tile + kWaves < tile_end ? load(tile + kWaves, fb) : false;
+    for (; tile < tile_end; tile += 2 * kWaves) {
+        if (oka) process(fa, tile);
+        oka = tile + 2 * kWaves < tile_end ? load(tile + 2 * kWaves, fa) : false;
+        if (tile + kWaves >= tile_end) break;
+        if (okb) process(fb, tile + kWaves);
+        okb = tile + 3 * kWaves < tile_end ? load(tile + 3 * kWaves, fb) : false;
     }
 
     // ---- wave result: column n < GW holds head n; lane (g, n) has d = 16j + 4g + r ----
@@ -333,7 +344,11 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
 
 template <int D, int GW>
 void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((decode_mfma_f16<D, GW>), grid, dim3(256), 0, s, p);
+    if (p.block_tokens == 16) {
+        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 16>), grid, dim3(256), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0>), grid, dim3(256), 0, s, p);
+    }
 }
 
 template <int D>

@@ -383,17 +383,19 @@ struct AppendParams {
     uint32_t num_blocks;
 };
 
-// One work item = one group of 32 elements of one token-head row of K or V.
+// One work item = EPT consecutive elements of one token-head row of K or V: a whole
+// 32-element quantisation group for int4 pools, 8 elements (16 or 32 bytes) otherwise.
 template <int DT, int SRC>
 __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
-    const uint32_t groups = p.head_dim / 32;
-    const uint64_t total = (uint64_t)p.batch * p.n_new * p.hkv * groups * 2;
+    constexpr int EPT = DT == VSPEC_KV_INT4 ? 32 : 8;
+    const uint32_t chunks = p.head_dim / EPT;
+    const uint64_t total = (uint64_t)p.batch * p.n_new * p.hkv * chunks * 2;
     for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
          it += (uint64_t)gridDim.x * blockDim.x) {
         const int which = (int)(it & 1);
         uint64_t r = it >> 1;
-        const uint32_t g = (uint32_t)(r % groups);
-        r /= groups;
+        const uint32_t c = (uint32_t)(r % chunks);
+        r /= chunks;
         const uint32_t h = (uint32_t)(r % p.hkv);
         r /= p.hkv;
         const uint32_t i = (uint32_t)(r % p.n_new);
@@ -406,60 +408,56 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
         if (lb >= p.max_blocks) continue;
         const int32_t phys = p.block_tables[(size_t)b * p.max_blocks + lb];
         if (phys < 0 || (uint32_t)phys >= p.num_blocks) continue;
-        const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + pos % p.block_tokens;
-        const size_t src_el = (((size_t)b * p.n_new + i) * p.hkv + h) * p.head_dim + (size_t)g * 32;
+        const uint32_t slot = pos % p.block_tokens;
+        const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + slot;
+        const size_t e0 = (size_t)c * EPT;  // first element of this chunk within the row
+        const size_t src_el = (((size_t)b * p.n_new + i) * p.hkv + h) * p.head_dim + e0;
 
-        float x[32];
+        float x[EPT];
         const uint8_t* src = which ? p.v_new : p.k_new;
         if constexpr (SRC == VSPEC_KV_F32) {
             const float4* s4 = reinterpret_cast<const float4*>(src + src_el * 4);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < EPT / 4; ++j) {
                 const float4 w = s4[j];
                 x[4 * j] = w.x; x[4 * j + 1] = w.y; x[4 * j + 2] = w.z; x[4 * j + 3] = w.w;
             }
         } else {
             const uint4* s4 = reinterpret_cast<const uint4*>(src + src_el * 2);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) unpack_f16x8(s4[j], x + 8 * j);
+            for (int j = 0; j < EPT / 8; ++j) unpack_f16x8(s4[j], x + 8 * j);
         }
 
         uint8_t* dst = which ? p.v : p.k;
         if constexpr (DT == VSPEC_KV_F32) {
-            float4* d4 = reinterpret_cast<float4*>(dst + (row * p.head_dim + (size_t)g * 32) * 4);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) d4[j] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+            float4* d4 = reinterpret_cast<float4*>(dst + (row * p.head_dim + e0) * 4);
+            d4[0] = make_float4(x[0], x[1], x[2], x[3]);
+            d4[1] = make_float4(x[4], x[5], x[6], x[7]);
         } else if constexpr (DT == VSPEC_KV_F16) {
-            if (which) {
-                // V tiles are d-major: element (d, slot) at tile + d*P + slot
-                const size_t tile = ((size_t)phys * p.hkv + h) * p.head_dim * p.block_tokens;
-                uint16_t* vt = reinterpret_cast<uint16_t*>(dst) + tile + pos % p.block_tokens;
-                const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src + src_el * 2);
-#pragma unroll
-                for (int e = 0; e < 32; ++e) {
-                    const size_t d = (size_t)g * 32 + e;
-                    vt[d * p.block_tokens] =
-                        SRC == VSPEC_KV_F16 ? s16[e] : (uint16_t)float_to_half_bits(x[e]);
-                }
-                continue;
-            }
-            uint4* d4 = reinterpret_cast<uint4*>(dst + (row * p.head_dim + (size_t)g * 32) * 2);
+            uint32_t hb[8];
             if constexpr (SRC == VSPEC_KV_F16) {
                 // pure copy of the source bits
-                const uint4* s4 = reinterpret_cast<const uint4*>(src + src_el * 2);
+                const uint4 w = *reinterpret_cast<const uint4*>(src + src_el * 2);
+                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) d4[j] = s4[j];
+                for (int k = 0; k < 4; ++k) {
+                    hb[2 * k] = ws[k] & 0xffffu;
+                    hb[2 * k + 1] = ws[k] >> 16;
+                }
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t w[4];
+                for (int k = 0; k < 8; ++k) hb[k] = float_to_half_bits(x[k]);
+            }
+            if (which) {
+                // V tiles are d-major: element (d, slot) at tile + d*P + slot
+                uint16_t* vt = reinterpret_cast<uint16_t*>(dst) +
+                               ((size_t)phys * p.hkv + h) * p.head_dim * p.block_tokens + slot;
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        w[k] = float_to_half_bits(x[8 * j + 2 * k]) |
-                               (float_to_half_bits(x[8 * j + 2 * k + 1]) << 16);
-                    }
-                    d4[j] = make_uint4(w[0], w[1], w[2], w[3]);
-                }
+                for (int k = 0; k < 8; ++k) vt[(e0 + k) * p.block_tokens] = (uint16_t)hb[k];
+            } else {
+                *reinterpret_cast<uint4*>(dst + (row * p.head_dim + e0) * 2) =
+                    make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16),
+                               hb[6] | (hb[7] << 16));
             }
         } else {
             // int4 codec: rep = 2nd-largest |x|, scale = rep/8 (1 if rep == 0),
@@ -487,10 +485,10 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
                 const int code = rr > 7.0f ? 7 : (rr >= -8.0f ? (int)rr : -8);
                 w[e / 8] |= ((uint32_t)code & 0xfu) << (4 * (e % 8));
             }
-            uint4* d4 = reinterpret_cast<uint4*>(dst + row * (p.head_dim / 2) + (size_t)g * 16);
+            uint4* d4 = reinterpret_cast<uint4*>(dst + row * (p.head_dim / 2) + e0 / 2);
             *d4 = make_uint4(w[0], w[1], w[2], w[3]);
             uint16_t* sd = which ? p.vs : p.ks;
-            sd[row * groups + g] = (uint16_t)s16;
+            sd[row * (p.head_dim / 32) + c] = (uint16_t)s16;
         }
     }
 }
@@ -895,7 +893,8 @@ int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* 
     p.block_tokens = kv->block_tokens;
     p.max_blocks = max_blocks_per_seq;
     p.num_blocks = kv->num_blocks;
-    const uint64_t items = (uint64_t)batch * n_new * kv->num_kv_heads * (kv->head_dim / 32) * 2;
+    const uint32_t ept = kv->dtype == VSPEC_KV_INT4 ? 32 : 8;
+    const uint64_t items = (uint64_t)batch * n_new * kv->num_kv_heads * (kv->head_dim / ept) * 2;
     uint64_t blocks = (items + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     const dim3 grid((unsigned)blocks);
