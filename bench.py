@@ -29,10 +29,13 @@ METRIC = "paged decode-attn tokens/s + achieved HBM GB/s (% of peak), Qwen3-8B K
 PEAK_GBS = 8000.0
 
 WORKLOADS = {
-    # name: (batch, ctx, q_heads, kv_heads, head_dim, block_tokens, kv dtype)
+    # T: uniform context; ctx_range: seeded U[lo, hi] per sequence with a pool of 1.2x the
+    # needed blocks (continuous batching); flow: the chunked-prefill/evict/compact flow
     "qwen3-8b-b64-ctx4k": dict(B=64, T=4097, Hq=32, Hkv=8, D=128, P=16, dtype="f16"),
     "qwen3-8b-b16-ctx2k": dict(B=16, T=2049, Hq=32, Hkv=8, D=128, P=16, dtype="f16"),
     "qwen3-8b-b16-ctx2k-int4": dict(B=16, T=2049, Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
+    "qwen3-8b-b64-ctx128-8k": dict(B=64, ctx_range=(128, 8192), Hq=32, Hkv=8, D=128, P=16, dtype="f16"),
+    "qwen3-8b-b8-chunk512-evict-int4": dict(B=8, flow="c5", Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
 }
 
 
@@ -57,7 +60,11 @@ def cpu_baseline(args, wl, pool, tables, ctx, q_all, out_gpu, mode):
 
     sys.path.insert(0, str(ROOT))
     S = min(args.cpu_seqs, wl["B"])
-    T, Hq, Hkv, D = wl["T"], wl["Hq"], wl["Hkv"], wl["D"]
+    Hq, Hkv, D = wl["Hq"], wl["Hkv"], wl["D"]
+    lens = [int(t) for t in ctx[:S].cpu().tolist()]
+    if len(set(lens)) > 1:
+        return cpu_baseline_ragged(wl, pool, tables, ctx, q_all, out_gpu, mode, S, lens)
+    T = lens[0]
     k, v, _, _ = vr.kv_gather(pool, tables[:S], ctx[:S], out_mode=vr.GATHER_F32)
     k = k.cpu().numpy().reshape(S, T, Hkv, D)
     v = v.cpu().numpy().reshape(S, T, Hkv, D)
@@ -98,6 +105,31 @@ def cpu_baseline(args, wl, pool, tables, ctx, q_all, out_gpu, mode):
     return res
 
 
+def cpu_baseline_ragged(wl, pool, tables, ctx, q_all, out_gpu, mode, S, lens):
+    """Reference CPU decode step, one sequence at a time (per-sequence context lengths)."""
+    import numpy as np
+
+    import vspec_rocm as vr
+    from oracle.oracle import REF_SO, Reference
+
+    if not REF_SO.exists():
+        return None
+    ref = Reference()
+    Hkv, D = wl["Hkv"], wl["D"]
+    sec, err = 0.0, 0.0
+    for b in range(S):
+        k, v, _, _ = vr.kv_gather(pool, tables[b:b + 1], ctx[b:b + 1], out_mode=vr.GATHER_F32)
+        k = k.cpu().numpy().reshape(1, lens[b], Hkv, D)
+        v = v.cpu().numpy().reshape(1, lens[b], Hkv, D)
+        s_b, out = ref.baseline_decode(mode, 1, k, v, q_all[b:b + 1].cpu().numpy(), wl["P"])
+        sec += s_b
+        err = max(err, float(np.abs(out[0] - out_gpu[b].cpu().numpy()).max()))
+    return {"value": S / sec, "unit": "tokens/s", "cores": 1, "kind": "reference",
+            "sample": f"{S} of {wl['B']} sequences (contexts {min(lens)}..{max(lens)}): reference decode "
+                      f"step (paged append + capi.c gather + attention_ref, numerics {'R' if mode else 'P'}), 1 thread",
+            "parity_max_abs_vs_gpu": err}
+
+
 def load_traffic(workload):
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
@@ -107,6 +139,118 @@ def load_traffic(workload):
         return t.get(workload, {}).get("hbm_bytes_per_launch")
     except (ValueError, OSError):
         return None
+
+
+def run_c5(args, wl, kv_dtype, mode):
+    """Config 5: 8 sequences with int4 contexts L0 ~ U[16384, 32256] (seeded) each append a
+    512-token fp16 chunk through quantize-on-write, evict the oldest 25 % of their blocks,
+    have the survivors compacted into fresh contiguous blocks, then decode.  Each stage is
+    timed with HIP events; the whole flow is one step."""
+    import ctypes as C
+
+    import torch
+
+    import vspec_rocm as vr
+
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, P, chunk = wl["B"], wl["Hq"], wl["Hkv"], wl["D"], wl["P"], 512
+    gc = torch.Generator().manual_seed(args.seed)
+    L0 = torch.randint(16384, 32256 + 1, (B,), generator=gc)
+    total = L0 + chunk
+    nb = (total + P - 1) // P
+    ev = nb * 25 // 100
+    surv = nb - ev
+    used = int(nb.sum())
+    num_blocks = used + int(surv.sum())
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    pool = vr.PagedPool(kv_dtype, num_blocks, P, Hkv, D, device=dev)
+    perm = torch.randperm(used, generator=g, device=dev).to(torch.int32)
+    tab = torch.full((B, int(nb.max())), -1, dtype=torch.int32, device=dev)
+    off = 0
+    for b in range(B):
+        tab[b, : nb[b]] = perm[off: off + int(nb[b])]
+        off += int(nb[b])
+    # initial contexts (setup, untimed): quantize-on-write appends in 512-token chunks
+    for s0 in range(0, int(L0.max()), chunk):
+        live = [b for b in range(B) if int(L0[b]) >= s0 + chunk]
+        if live:
+            li = torch.tensor(live, device=dev)
+            kk = torch.randn((len(live), chunk, Hkv, D), generator=g, device=dev, dtype=torch.float16)
+            vv = torch.randn((len(live), chunk, Hkv, D), generator=g, device=dev, dtype=torch.float16)
+            vr.kv_append(pool, tab[li].contiguous(), torch.full((len(live),), s0, dtype=torch.int32, device=dev), kk, vv)
+    for b in range(B):
+        s0 = int(L0[b]) // chunk * chunk
+        n = int(L0[b]) - s0
+        if n:
+            kk = torch.randn((1, n, Hkv, D), generator=g, device=dev, dtype=torch.float16)
+            vv = torch.randn((1, n, Hkv, D), generator=g, device=dev, dtype=torch.float16)
+            vr.kv_append(pool, tab[b:b + 1], torch.tensor([s0], dtype=torch.int32, device=dev), kk, vv)
+    kc = torch.randn((B, chunk, Hkv, D), generator=g, device=dev, dtype=torch.float16)
+    vc = torch.randn((B, chunk, Hkv, D), generator=g, device=dev, dtype=torch.float16)
+    start = L0.to(torch.int32).to(dev)
+    src = torch.cat([tab[b, int(ev[b]): int(nb[b])] for b in range(B)]).contiguous()
+    base = used + torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(surv, 0)[:-1]])
+    dst = torch.cat([base[b] + torch.arange(int(surv[b])) for b in range(B)]).to(torch.int32).to(dev)
+    new_tab = torch.full((B, int(surv.max())), -1, dtype=torch.int32)
+    for b in range(B):
+        new_tab[b, : surv[b]] = base[b] + torch.arange(int(surv[b]))
+    new_tab = new_tab.to(dev)
+    new_ctx = (total - ev * P).to(torch.int32).to(dev)
+    q = torch.randn((B, Hq, D), generator=g, device=dev, dtype=torch.float32)
+    out = torch.empty_like(q)
+    desc = vr.make_decode_desc(pool, new_tab, new_ctx, q, out, int(new_ctx.max()), mode)
+    ws = torch.empty(max(vr.decode_workspace_bytes(desc), 4), dtype=torch.uint8, device=dev)
+    desc.workspace, desc.workspace_bytes = ws.data_ptr(), ws.numel()
+    L = vr.lib()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+
+    def flow(e):
+        if e:
+            e[0].record()
+        vr.kv_append(pool, tab, start, kc, vc)
+        if e:
+            e[1].record()
+        vr.kv_compact(pool, src, dst)
+        if e:
+            e[2].record()
+        if not L.vspec_rocm_paged_decode_attention(C.byref(desc)):
+            raise vr.VspecRocmError(vr.last_error())
+        if e:
+            e[3].record()
+
+    for _ in range(args.warmup):
+        flow(None)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        flow(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    stage = [sum(e[k].elapsed_time(e[k + 1]) for e in evs) / args.steps / 1e3 for k in range(3)]
+    row = Hkv * (2 * (D // 2 + 2 * (D // 32)))  # K+V int4 bytes per token (codes + scales)
+    append_bytes = B * chunk * (Hkv * D * 2 * 2 + row)          # fp16 in, int4 out
+    compact_bytes = 2 * int(surv.sum()) * P * row                 # read + write survivors
+    ctxs = new_ctx.cpu().tolist()
+    decode_bytes = algorithmic_bytes(ctxs, Hq, Hkv, D, P, "int4")
+    gbs = lambda n, t: n / t / 1e9
+    return {
+        "metric": METRIC, "value": B * args.steps / wall, "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: seeded N(0,1) fp16 tokens quantised to int4 on write",
+        "config": {"workload": args.workload, "batch": B, "ctx": [min(ctxs), max(ctxs)], "chunk": chunk,
+                   "evict": "oldest 25% of blocks", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
+                   "block_tokens": P, "kv_storage": "int4", "numerics": args.numerics, "parallelism": "single-gpu"},
+        "stages": {
+            "chunk_append": {"ms": stage[0] * 1e3, "GB/s": gbs(append_bytes, stage[0])},
+            "compact": {"ms": stage[1] * 1e3, "GB/s": gbs(compact_bytes, stage[1]), "blocks": int(surv.sum())},
+            "decode": {"ms": stage[2] * 1e3, "GB/s": gbs(decode_bytes, stage[2]), "tokens_per_s": B / stage[2]},
+        },
+        "roofline": {"bound": "hbm", "achieved": gbs(decode_bytes, stage[2]), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs(decode_bytes, stage[2]) / PEAK_GBS, "traffic": load_traffic(args.workload),
+                     "kernel": "decode_partial (int4)", "algorithmic_bytes_per_launch": decode_bytes},
+    }
 
 
 def main():
@@ -135,25 +279,46 @@ def main():
     vr.lib()
     dev = torch.device("cuda:0")
     wl = WORKLOADS[args.workload]
-    B, T, Hq, Hkv, D, P = wl["B"], wl["T"], wl["Hq"], wl["Hkv"], wl["D"], wl["P"]
     kv_dtype = {"f16": vr.KV_F16, "f32": vr.KV_F32, "int4": vr.KV_INT4}[wl["dtype"]]
     mode = vr.NUMERICS_3BIT if args.numerics == "R" else vr.NUMERICS_PLAIN
-    nblk = (T + P - 1) // P
+    if wl.get("flow") == "c5":
+        print(json.dumps(run_c5(args, wl, kv_dtype, mode)), flush=True)
+        return
+    B, Hq, Hkv, D, P = wl["B"], wl["Hq"], wl["Hkv"], wl["D"], wl["P"]
+    if "ctx_range" in wl:
+        lo, hi = wl["ctx_range"]
+        gc = torch.Generator().manual_seed(args.seed)
+        lens = torch.randint(lo, hi + 1, (B,), generator=gc).tolist()
+    else:
+        lens = [wl["T"]] * B
+    T = max(lens)
+    nblks = [(t + P - 1) // P for t in lens]
+    nblk = max(nblks)
+    pool_blocks = sum(nblks) if "ctx_range" not in wl else -(-sum(nblks) * 6 // 5)
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed)
 
     # pools smaller than the 256 MB MALL are rotated through >= 4 copies (>= 1 GB total)
-    per_pool = vr.lib().vspec_rocm_kv_pool_bytes(kv_dtype, B * nblk, P, Hkv, D)
+    per_pool = vr.lib().vspec_rocm_kv_pool_bytes(kv_dtype, pool_blocks, P, Hkv, D)
     copies = 1 if per_pool >= (1 << 30) else max(4, -(-(1 << 30) // per_pool))
-    log(f"workload {args.workload}: B={B} ctx={T} GQA {Hq}/{Hkv} D={D} P={P} {wl['dtype']} "
+    log(f"workload {args.workload}: B={B} ctx={min(lens)}..{T} GQA {Hq}/{Hkv} D={D} P={P} {wl['dtype']} "
         f"pool {per_pool / 1e9:.3f} GB x {copies}")
+
+    def make_table():
+        perm = torch.randperm(pool_blocks, generator=g, device=dev).to(torch.int32)
+        tab = torch.full((B, nblk), -1, dtype=torch.int32, device=dev)
+        off = 0
+        for b in range(B):
+            tab[b, : nblks[b]] = perm[off: off + nblks[b]]
+            off += nblks[b]
+        return tab
 
     pools, tables_l = [], []
     for c in range(copies):
-        pool = vr.PagedPool(kv_dtype, B * nblk, P, Hkv, D, device=dev)
+        pool = vr.PagedPool(kv_dtype, pool_blocks, P, Hkv, D, device=dev)
         if kv_dtype == vr.KV_INT4:
             # build the cache by quantize-on-write appends of fp16 N(0,1) tokens
-            tab = torch.randperm(B * nblk, generator=g, device=dev).to(torch.int32).view(B, nblk)
+            tab = make_table()
             chunk = 512
             for s0 in range(0, T, chunk):
                 n = min(chunk, T - s0)
@@ -163,11 +328,11 @@ def main():
         else:
             pool.k.copy_(torch.randn(pool.k.shape, generator=g, device=dev, dtype=torch.float32).to(pool.k.dtype))
             pool.v.copy_(torch.randn(pool.v.shape, generator=g, device=dev, dtype=torch.float32).to(pool.v.dtype))
-            tab = torch.randperm(B * nblk, generator=g, device=dev).to(torch.int32).view(B, nblk)
+            tab = make_table()
         pools.append(pool)
         tables_l.append(tab)
-    ctx = torch.full((B,), T, dtype=torch.int32, device=dev)
-    pos = torch.full((B,), T - 1, dtype=torch.int32, device=dev)
+    ctx = torch.tensor(lens, dtype=torch.int32, device=dev)
+    pos = ctx - 1
     q = torch.randn((B, Hq, D), generator=g, device=dev, dtype=torch.float32)
     k_new = torch.randn((B, 1, Hkv, D), generator=g, device=dev, dtype=torch.float16)
     v_new = torch.randn((B, 1, Hkv, D), generator=g, device=dev, dtype=torch.float16)
@@ -208,7 +373,7 @@ def main():
     avg_attn_s = sum(attn_ms) / len(attn_ms) / 1e3
     med_attn_ms = attn_ms[len(attn_ms) // 2]
 
-    alg = algorithmic_bytes([T] * B, Hq, Hkv, D, P, wl["dtype"])
+    alg = algorithmic_bytes(lens, Hq, Hkv, D, P, wl["dtype"])
     achieved = alg / avg_attn_s / 1e9
     traffic = load_traffic(args.workload)
 
@@ -225,7 +390,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: seeded N(0,1) K/V resident in HBM, random-permutation block tables",
-        "config": {"workload": args.workload, "batch": B, "ctx": T, "q_heads": Hq, "kv_heads": Hkv,
+        "config": {"workload": args.workload, "batch": B, "ctx": T if min(lens) == T else [min(lens), T],
+                   "q_heads": Hq, "kv_heads": Hkv,
                    "head_dim": D, "block_tokens": P, "kv_storage": wl["dtype"], "numerics": args.numerics,
                    "pool_copies": copies, "parallelism": "single-gpu"},
         "attention_only": {"tokens_per_s": B / avg_attn_s, "avg_ms": avg_attn_s * 1e3, "median_ms": med_attn_ms,
@@ -242,7 +408,9 @@ def main():
         if not L.vspec_rocm_paged_decode_attention(C.byref(descs[0])):
             raise vr.VspecRocmError(vr.last_error())
         torch.cuda.synchronize()
-        result["cpu_baseline"] = cpu_baseline(args, wl, pools[0], tables_l[0], ctx, q, out, mode)
+        cb = cpu_baseline(args, wl, pools[0], tables_l[0], ctx, q, out, mode)
+        if cb is not None:
+            result["cpu_baseline"] = cb
     print(json.dumps(result), flush=True)
 
 

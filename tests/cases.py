@@ -95,3 +95,34 @@ def continuous_c4(oracle, B=64, lo=128, hi=8192, seed=4, dtype=DTYPE_F16):
     ctx = oracle.uniform_int(seed, lo, hi, B)
     need = int(((ctx + 15) // 16).sum())
     return make_case(oracle, dtype, B, 32, 8, 128, 16, ctx, seed, num_blocks=int(np.ceil(1.2 * need)))
+
+
+def chunk_evict_c5(oracle, lo=16384, hi=32256, B=8, chunk=512, seed=5, P=16):
+    """Config 5 semantics: each sequence holds an int4 context of L0 ~ U[lo, hi] tokens,
+    appends one `chunk`-token fp16 chunk through quantize-on-write, evicts its oldest
+    floor(25%) logical blocks, and has its surviving blocks compacted into a fresh
+    contiguous run of physical blocks.  Returns the plan (numpy, host side)."""
+    L0 = oracle.uniform_int(seed, lo, hi, B)
+    total = L0 + chunk
+    nb = (total + P - 1) // P
+    ev = (nb * 25) // 100
+    surv = nb - ev
+    # physical blocks: the live cache is a seeded permutation of the first sum(nb) blocks;
+    # compaction destinations are a contiguous region after them
+    used = int(nb.sum())
+    perm = oracle.permutation(seed ^ 0xC5, used)
+    tables = np.full((B, int(nb.max())), -1, np.int32)
+    off = 0
+    for b in range(B):
+        tables[b, : nb[b]] = perm[off: off + nb[b]]
+        off += nb[b]
+    dst_base = used + np.concatenate([[0], np.cumsum(surv)[:-1]]).astype(np.int32)
+    src = np.concatenate([tables[b, ev[b]: nb[b]] for b in range(B)]).astype(np.int32)
+    dst = np.concatenate([dst_base[b] + np.arange(surv[b]) for b in range(B)]).astype(np.int32)
+    new_tables = np.full((B, int(surv.max())), -1, np.int32)
+    for b in range(B):
+        new_tables[b, : surv[b]] = dst_base[b] + np.arange(surv[b])
+    new_ctx = (total - ev * P).astype(np.int32)
+    return dict(L0=L0.astype(np.int32), total=total.astype(np.int32), nb=nb, ev=ev, tables=tables,
+                num_blocks=used + int(surv.sum()), src=src, dst=dst, new_tables=new_tables,
+                new_ctx=new_ctx)

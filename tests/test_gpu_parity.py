@@ -300,3 +300,70 @@ def test_decode_partition_invariance(oracle, gpu):
     for o in outs[1:]:
         assert np.abs(o - outs[0]).max() < 1e-5
     check_attention(oracle, case, outs[0], 0)
+
+
+# ----------------------------------------------------------------------------- config 5
+@pytest.mark.parametrize("mode", [0, 1])
+def test_config5_chunk_evict_compact(oracle, gpu, mode):
+    """C5 at reduced context: int4 contexts, a 512-token fp16 chunk appended with
+    quantize-on-write, oldest 25% of blocks evicted, survivors compacted, decode."""
+    import torch
+    import vspec_rocm as vr
+    from cases import chunk_evict_c5
+
+    say(f"[c5] mode={mode} build")
+    plan = chunk_evict_c5(oracle, lo=1000, hi=2600, seed=55 + mode)
+    B, Hq, Hkv, D, P, chunk = 8, 32, 8, 128, 16, 512
+    host = HostPool(DTYPE_INT4, plan["num_blocks"], P, Hkv, D)
+    from cases import fill_garbage
+    fill_garbage(host)
+    case = type("C", (), {})()
+    case.dtype, case.num_blocks, case.P, case.Hkv, case.D = DTYPE_INT4, plan["num_blocks"], P, Hkv, D
+    pool = device_pool(case, gpu)
+    tab_d = torch.from_numpy(plan["tables"]).to(gpu)
+    Lmax = int(plan["L0"].max())
+    # initial contexts: appended in 512-token chunks (sequences shorter than a chunk
+    # boundary append only their own tokens)
+    ks = oracle.f32_to_f16(oracle.normal(501 + mode, B * (Lmax + chunk) * Hkv * D).reshape(B, Lmax + chunk, Hkv, D))
+    vs = oracle.f32_to_f16(oracle.normal(601 + mode, B * (Lmax + chunk) * Hkv * D).reshape(B, Lmax + chunk, Hkv, D))
+    k_d = _np_to_dev(ks, gpu)
+    v_d = _np_to_dev(vs, gpu)
+    for s0 in range(0, Lmax, chunk):
+        live = np.flatnonzero(plan["L0"] >= s0 + chunk)
+        if live.size:
+            oracle.paged_append(host, np.ascontiguousarray(plan["tables"][live]), np.full(live.size, s0, np.int32),
+                                np.ascontiguousarray(ks[live, s0:s0 + chunk]), np.ascontiguousarray(vs[live, s0:s0 + chunk]))
+            li = torch.from_numpy(live).to(gpu)
+            vr.kv_append(pool, tab_d[li].contiguous(), torch.full((live.size,), s0, dtype=torch.int32, device=gpu),
+                         k_d[li, s0:s0 + chunk].contiguous(), v_d[li, s0:s0 + chunk].contiguous())
+    for b in range(B):  # ragged remainder of each initial context, one sequence at a time
+        s0 = (int(plan["L0"][b]) // chunk) * chunk
+        n = int(plan["L0"][b]) - s0
+        if n:
+            oracle.paged_append(host, np.ascontiguousarray(plan["tables"][b:b + 1]), np.array([s0], np.int32),
+                                np.ascontiguousarray(ks[b:b + 1, s0:s0 + n]), np.ascontiguousarray(vs[b:b + 1, s0:s0 + n]))
+            vr.kv_append(pool, tab_d[b:b + 1], torch.tensor([s0], dtype=torch.int32, device=gpu),
+                         k_d[b:b + 1, s0:s0 + n].contiguous(), v_d[b:b + 1, s0:s0 + n].contiguous())
+    torch.cuda.synchronize()
+    say("[c5] chunk append")
+    # the chunked-prefill append: every sequence appends 512 tokens at its own position
+    kc = np.stack([ks[b, plan["L0"][b]: plan["L0"][b] + chunk] for b in range(B)])
+    vc = np.stack([vs[b, plan["L0"][b]: plan["L0"][b] + chunk] for b in range(B)])
+    assert oracle.paged_append(host, plan["tables"], plan["L0"], np.ascontiguousarray(kc), np.ascontiguousarray(vc))
+    vr.kv_append(pool, tab_d, torch.from_numpy(plan["L0"]).to(gpu), _np_to_dev(kc, gpu), _np_to_dev(vc, gpu))
+    torch.cuda.synchronize()
+    assert_pools_equal(host, pool)
+    say("[c5] evict + compact")
+    assert oracle.paged_compact(host, plan["src"], plan["dst"])
+    vr.kv_compact(pool, torch.from_numpy(plan["src"]).to(gpu), torch.from_numpy(plan["dst"]).to(gpu))
+    torch.cuda.synchronize()
+    assert_pools_equal(host, pool)
+    say("[c5] decode")
+    q = oracle.normal(701 + mode, B * Hq * D).reshape(B, Hq, D)
+    out = vr.paged_decode(pool, torch.from_numpy(plan["new_tables"]).to(gpu), torch.from_numpy(plan["new_ctx"]).to(gpu),
+                          torch.from_numpy(q).to(gpu), max_ctx_len=int(plan["new_ctx"].max()), numerics=mode)
+    torch.cuda.synchronize()
+    want = oracle.paged_decode(mode, host, plan["new_tables"], plan["new_ctx"], q)
+    err = float(np.abs(out.cpu().numpy() - want).max())
+    assert err <= TOL[DTYPE_INT4], err
+    say(f"[c5] max-abs {err:.2e}")
