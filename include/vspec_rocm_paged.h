@@ -1,0 +1,98 @@
+/*
+ * vspec_rocm_paged.h -- session/page bookkeeping of the paged KV cache and the
+ * GPU-resident handle API that Vspec's Python runtime binds with ctypes.
+ *
+ * 1. VspecRocmPagedMeta: the reference allocator (kv_paged_cache.c) restated on the
+ *    host with its exact policy -- first-fit page allocation, whole-session LRU
+ *    eviction on exhaustion, reference-counted prefix sharing, per-page used counts,
+ *    the clock -- but with the caps lifted (page ids are uint32, limits are chosen at
+ *    creation; 0 selects the reference's 128 sessions / 1024 pages per session).
+ *    It only decides where tokens live; the data lives in a VspecPagedKV pool.
+ *
+ * 2. vspec_py_kv_cache_*: the paged-KV section of the reference's Python C-API
+ *    (capi.h:46-57, capi.c:2188-2299) with identical signatures, backed by an HBM f32
+ *    pool.  A ctypes loader that points at libvspec_rocm.so instead of
+ *    libvspec_engine_capi runs CorePagedKVCache (runtime_core_bridge.py:479-549)
+ *    unchanged.
+ */
+#ifndef VSPEC_ROCM_PAGED_H
+#define VSPEC_ROCM_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "vspec_rocm.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same fields and order as VspecKVPagedStats (kv_paged_cache.h:11-18). */
+typedef struct VspecRocmPagedStats {
+    uint64_t page_alloc_count;
+    uint64_t page_reuse_count;
+    uint64_t evict_session_count;
+    uint64_t append_token_count;
+    size_t free_pages;
+    size_t active_sessions;
+} VspecRocmPagedStats;
+
+typedef struct VspecRocmPagedMeta VspecRocmPagedMeta; /* opaque */
+
+/* vspec_kv_paged_cache_init (kv_paged_cache.c:124-149); returns NULL on bad arguments. */
+VspecRocmPagedMeta* vspec_rocm_paged_meta_create(size_t page_tokens, size_t max_pages,
+                                                 size_t max_sessions,
+                                                 size_t max_pages_per_session);
+void vspec_rocm_paged_meta_destroy(VspecRocmPagedMeta* m);
+/* Back to the state right after creation (capi.c:2237-2245 reset). */
+void vspec_rocm_paged_meta_reset(VspecRocmPagedMeta* m);
+
+int vspec_rocm_paged_open_session(VspecRocmPagedMeta* m, uint64_t session_id);   /* :151-174 */
+int vspec_rocm_paged_close_session(VspecRocmPagedMeta* m, uint64_t session_id);  /* :176-183 */
+int vspec_rocm_paged_reuse_prefix(VspecRocmPagedMeta* m, uint64_t target_session_id,
+                                  uint64_t source_session_id, size_t max_tokens);  /* :185-241 */
+/* The bookkeeping of vspec_kv_paged_append (:243-310): reserves the next token of the
+ * session and returns its physical page and slot; the caller writes the data. */
+int vspec_rocm_paged_reserve(VspecRocmPagedMeta* m, uint64_t session_id, uint32_t* page,
+                             uint32_t* slot);
+/* vspec_kv_paged_get_token_ptr addressing (:312-356): page and slot of token_idx. */
+int vspec_rocm_paged_locate(const VspecRocmPagedMeta* m, uint64_t session_id, size_t token_idx,
+                            uint32_t* page, uint32_t* slot);
+size_t vspec_rocm_paged_session_tokens(const VspecRocmPagedMeta* m, uint64_t session_id);
+void vspec_rocm_paged_stats(const VspecRocmPagedMeta* m, VspecRocmPagedStats* out);  /* :366-384 */
+/* The session's page list (physical page ids in order); returns the page count. */
+size_t vspec_rocm_paged_session_pages(const VspecRocmPagedMeta* m, uint64_t session_id,
+                                      uint32_t* out, size_t cap);
+/* Page metadata: allocated flag, used tokens, reference count. */
+int vspec_rocm_paged_page_info(const VspecRocmPagedMeta* m, size_t page, uint32_t* allocated,
+                               uint32_t* used_tokens, uint32_t* ref_count);
+/* Block table for the decode kernel: pages in order when every page but the last is
+ * full (then *ctx_len = session tokens); returns 0 otherwise (prefix reuse left a
+ * partly filled page in the middle: gather rows instead). */
+int vspec_rocm_paged_block_table(const VspecRocmPagedMeta* m, uint64_t session_id, int32_t* out,
+                                 size_t cap, uint32_t* ctx_len);
+
+/* ---- GPU-resident handles with the reference Python C-API signatures ---- */
+int vspec_py_kv_cache_create(size_t page_tokens, size_t max_pages, size_t num_heads, size_t head_dim);
+void vspec_py_kv_cache_destroy(int handle_id);
+int vspec_py_kv_cache_reset(int handle_id);
+int vspec_py_kv_cache_append(int handle_id, uint64_t session_id, const float* key_token,
+                             const float* value_token);
+size_t vspec_py_kv_cache_session_tokens(int handle_id, uint64_t session_id);
+size_t vspec_py_kv_cache_read(int handle_id, uint64_t session_id, float* out_keys,
+                              float* out_values, size_t max_tokens);
+
+/* The handle's metadata and device pool, for callers that batch on the GPU. */
+VspecRocmPagedMeta* vspec_py_kv_cache_meta(int handle_id);
+const VspecPagedKV* vspec_py_kv_cache_pool(int handle_id);
+
+/* Gather explicit rows: token i of the output is (pages[i], slots[i]) of every head,
+ * written in [n][H][D] order as f32 (device pointers). */
+int vspec_rocm_kv_gather_rows(const VspecPagedKV* kv, uint32_t n, const int32_t* pages,
+                              const int32_t* slots, float* out_k, float* out_v, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -56,14 +56,25 @@ def test_argument_validation_without_gpu():
 
     L = vspec_rocm.lib()
     kv = vspec_rocm.VspecPagedKV()
-    kv.dtype, kv.num_blocks, kv.block_tokens, kv.num_kv_heads, kv.head_dim = 1, 4, 16, 2, 96
+    kv.dtype, kv.num_blocks, kv.block_tokens, kv.num_kv_heads, kv.head_dim = 1, 4, 16, 2, 12
     kv.k_data = kv.v_data = 0x1000
     assert L.vspec_rocm_kv_append(C.byref(kv), 1, 0x1, 1, 0x1, 1, 0x1, 0x1, 1, None) == 0
     assert "head_dim" in vspec_rocm.last_error()
-    kv.head_dim, kv.block_tokens = 128, 24
+    kv.dtype, kv.head_dim = 2, 48  # int4 rows are whole 32-element groups
     assert L.vspec_rocm_kv_append(C.byref(kv), 1, 0x1, 1, 0x1, 1, 0x1, 0x1, 1, None) == 0
+    assert "multiple of 32" in vspec_rocm.last_error()
+    kv.dtype = 1
+    # decode needs block_tokens % 16 == 0 and head_dim in {64, 128}; append and gather do not
+    dd = vspec_rocm.VspecPagedAttnDesc()
+    dd.batch, dd.num_q_heads = 1, 4
+    dd.kv = kv
+    dd.kv.head_dim, dd.kv.block_tokens = 128, 24
+    assert L.vspec_rocm_paged_decode_workspace_bytes(C.byref(dd)) == 0
     assert "block_tokens" in vspec_rocm.last_error()
-    kv.block_tokens, kv.dtype = 16, 2  # int4 without scales
+    dd.kv.head_dim, dd.kv.block_tokens = 96, 16
+    assert L.vspec_rocm_paged_decode_workspace_bytes(C.byref(dd)) == 0
+    assert "64 or 128" in vspec_rocm.last_error()
+    kv.head_dim, kv.block_tokens, kv.dtype = 128, 16, 2  # int4 without scales
     assert L.vspec_rocm_kv_gather(C.byref(kv), 1, 0x1, 1, 0x1, 16, 0x1, 0, 0x1, 0x1, None, None, None) == 0
     assert "scales" in vspec_rocm.last_error()
     d = vspec_rocm.VspecPagedAttnDesc()

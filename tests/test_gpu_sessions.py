@@ -1,0 +1,168 @@
+"""GPU parity of the session layer: the handle API (vspec_py_kv_cache_*) over HBM
+against the reference's own paged cache (kv_paged_cache.c compiled into oracle/_ref),
+driven through the same seeded operation sequence.  Reads are bit-exact; decode over a
+handle's pool through allocator-built block tables matches the reference's GQA
+attention over the same tokens to the fp32 bar (1e-4)."""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+_f32p = C.POINTER(C.c_float)
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    import torch
+    import vspec_rocm
+
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible for a gpu-marked test")
+    vspec_rocm.lib()
+    return torch.device("cuda:0")
+
+
+def _ref_read(ref, c, sid, H, D):
+    n = ref.lib.vspec_kv_paged_session_tokens(c, sid)
+    k = np.zeros((max(n, 1), H, D), np.float32)
+    v = np.zeros_like(k)
+    got = ref.lib.vr_paged_read(c, sid, k.ctypes.data_as(_f32p), v.ctypes.data_as(_f32p), 0)
+    return k[:got], v[:got]
+
+
+@pytest.mark.parametrize("P,MAXP,H,D,seed", [(16, 24, 2, 128, 1), (5, 13, 3, 12, 2), (32, 9, 1, 64, 3)])
+def test_handles_match_reference_cache(ref, gpu, P, MAXP, H, D, seed):
+    from vspec_rocm.sessions import CorePagedKVCache
+
+    say(f"[sessions] P={P} MAXP={MAXP} H={H} D={D} seed={seed}")
+    rng = np.random.default_rng(seed)
+    cache = CorePagedKVCache(P, MAXP, H, D)
+    c = ref.lib.vr_paged_new(P, MAXP, H, D)
+    ids = [int(x) for x in rng.integers(0, 7, 10)]
+    try:
+        for step in range(500):
+            op = int(rng.integers(0, 12))
+            a, b = int(rng.choice(ids)), int(rng.choice(ids))
+            if op <= 7:
+                k = rng.standard_normal((H, D)).astype(np.float32)
+                v = rng.standard_normal((H, D)).astype(np.float32)
+                r1 = cache.append(k, v, session_id=a)
+                r2 = ref.lib.vspec_kv_paged_append(c, a, k.ctypes.data_as(_f32p), v.ctypes.data_as(_f32p))
+                assert r1 == bool(r2), step
+            elif op == 8:
+                assert cache.open_session(a) == bool(ref.lib.vspec_kv_paged_open_session(c, a))
+            elif op == 9:
+                assert cache.close_session(a) == bool(ref.lib.vspec_kv_paged_close_session(c, a))
+            else:
+                mt = int(rng.integers(0, 3 * P))
+                assert cache.reuse_prefix(a, b, mt) == bool(ref.lib.vspec_kv_paged_reuse_prefix(c, a, b, mt))
+            if step % 50 == 49 or step == 499:
+                for s in sorted(set(ids)):
+                    assert cache.session_tokens(s) == ref.lib.vspec_kv_paged_session_tokens(c, s)
+                    wk, wv = _ref_read(ref, c, s, H, D)
+                    gk, gv = cache.read_tokens(session_id=s)
+                    if wk.shape[0] == 0:
+                        assert gk is not None and gk.shape[0] == 0
+                        continue
+                    assert gk.shape == wk.shape
+                    assert np.array_equal(gk.view(np.uint32), wk.view(np.uint32)), (step, s)
+                    assert np.array_equal(gv.view(np.uint32), wv.view(np.uint32)), (step, s)
+                    # a bounded read returns the prefix
+                    m = max(1, wk.shape[0] // 2)
+                    pk, _ = cache.read_tokens(max_tokens=m, session_id=s)
+                    assert np.array_equal(pk, wk[:m])
+        st = cache.stats()
+        out = (C.c_uint64 * 6)()
+        ref.lib.vr_paged_stats(c, out)
+        assert list(st.values()) == list(out)
+        say(f"[sessions] stats {st}")
+    finally:
+        cache.close()
+        ref.lib.vr_paged_free(c)
+
+
+def test_reset_and_handle_table(gpu):
+    from vspec_rocm import VspecRocmError, lib
+    from vspec_rocm.sessions import CorePagedKVCache
+
+    a = CorePagedKVCache(16, 4, 1, 8, session_id=5)
+    x = np.arange(8, dtype=np.float32)
+    for _ in range(20):
+        assert a.append(x, -x)
+    assert a.session_tokens() == 20
+    k, v = a.read_tokens()
+    assert np.array_equal(k[:, 0], np.tile(x, (20, 1))) and np.array_equal(v[:, 0], np.tile(-x, (20, 1)))
+    a.reset()
+    assert a.session_tokens() == 0
+    k, v = a.read_tokens()
+    assert k.shape == (0, 1, 8)
+    # 16 handles at most, as in the reference
+    extra = []
+    try:
+        while len(extra) < 20:
+            extra.append(CorePagedKVCache(16, 1, 1, 8))
+    except VspecRocmError:
+        pass
+    assert len(extra) == 15
+    for e in extra:
+        e.close()
+    a.close()
+    assert lib().vspec_py_kv_cache_append(a.handle, 5, None, None) == 0
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_decode_over_handle_pool(ref, gpu, mode):
+    """Sessions filled through the handle API, one sharing a page-aligned prefix;
+    block tables from the allocator; decode on the handle's f32 pool."""
+    import torch
+    import vspec_rocm as vr
+    from vspec_rocm.sessions import CorePagedKVCache
+
+    P, H, D, Hq = 16, 2, 64, 8
+    rng = np.random.default_rng(7 + mode)
+    lens = {1: 173, 2: 64, 3: 300, 4: 1}
+    cache = CorePagedKVCache(P, 64, H, D)
+    try:
+        for sid, n in lens.items():
+            for _ in range(n):
+                assert cache.append(rng.standard_normal((H, D)), rng.standard_normal((H, D)), session_id=sid)
+        # session 5 shares session 3's first 96 tokens (6 full pages), then grows
+        assert cache.reuse_prefix(5, 3, 96)
+        for _ in range(21):
+            assert cache.append(rng.standard_normal((H, D)), rng.standard_normal((H, D)), session_id=5)
+        # sharing whole pages up to 40 tokens takes 2 pages; sharing everything takes
+        # session 1's partly filled last page, which then sits in the middle of session 7
+        assert cache.reuse_prefix(6, 1, 40)
+        cache.append(rng.standard_normal((H, D)), rng.standard_normal((H, D)), session_id=6)
+        assert cache.block_table(6, 32)[1] == 33
+        assert cache.reuse_prefix(7, 1, 0)
+        cache.append(rng.standard_normal((H, D)), rng.standard_normal((H, D)), session_id=7)
+        assert cache.session_tokens(7) == 174
+        assert cache.block_table(7, 32) is None
+        sids = [1, 2, 3, 4, 5]
+        tabs, ctx = [], []
+        for s in sids:
+            t, n = cache.block_table(s, 32)
+            tabs.append(t)
+            ctx.append(n)
+        assert ctx == [173, 64, 300, 1, 117]
+        q = rng.standard_normal((len(sids), Hq, D)).astype(np.float32)
+        pool = cache.device_pool()
+        out = vr.paged_decode(pool, torch.from_numpy(np.stack(tabs)).to(gpu),
+                              torch.tensor(ctx, dtype=torch.int32, device=gpu), torch.from_numpy(q).to(gpu),
+                              numerics=mode)
+        got = out.cpu().numpy()
+        for i, s in enumerate(sids):
+            k, v = cache.read_tokens(session_id=s)
+            want = ref.attention_gqa(mode, q[i], k, v)
+            err = float(np.abs(got[i] - want).max())
+            assert err <= 1e-4, (s, err)
+    finally:
+        cache.close()

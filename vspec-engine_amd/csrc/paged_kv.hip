@@ -16,7 +16,7 @@
 #include <stdio.h>
 #include <string.h>
 
-#include "vspec_rocm.h"
+#include "vspec_rocm_paged.h"
 
 // ---------------------------------------------------------------------------
 // error reporting
@@ -598,6 +598,68 @@ __global__ __launch_bounds__(256) void kv_gather(GatherParams p) {
     }
 }
 
+struct GatherRowsParams {
+    const uint8_t* k;
+    const uint8_t* v;
+    const uint16_t* ks;
+    const uint16_t* vs;
+    const int32_t* pages;
+    const int32_t* slots;
+    float* ok;
+    float* ov;
+    uint32_t n;
+    uint32_t hkv;
+    uint32_t head_dim;
+    uint32_t block_tokens;
+    uint32_t num_blocks;
+};
+
+// Row-list gather to f32: output token i is (pages[i], slots[i]) of every head, [n][H][D].
+// One thread per 8 elements of one row of K or V.
+template <int DT>
+__global__ __launch_bounds__(256) void kv_gather_rows(GatherRowsParams p) {
+    const uint32_t D = p.head_dim, P = p.block_tokens;
+    const uint32_t cpr = D / 8;
+    const uint64_t total = (uint64_t)p.n * p.hkv * cpr * 2;
+    for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
+         it += (uint64_t)gridDim.x * blockDim.x) {
+        const int which = (int)(it & 1);
+        uint64_t r = it >> 1;
+        const uint32_t c = (uint32_t)(r % cpr);
+        r /= cpr;
+        const uint32_t h = (uint32_t)(r % p.hkv);
+        const uint32_t i = (uint32_t)(r / p.hkv);
+        const int32_t page = p.pages[i], slot = p.slots[i];
+        if (page < 0 || (uint32_t)page >= p.num_blocks || slot < 0 || (uint32_t)slot >= P) continue;
+        const size_t tile = (size_t)page * p.hkv + h;
+        const size_t row = tile * P + slot;
+        const uint8_t* src = which ? p.v : p.k;
+        float x[8];
+        if constexpr (DT == VSPEC_KV_F32) {
+            const float4* s4 = reinterpret_cast<const float4*>(src + row * D * 4) + 2 * c;
+            const float4 a = s4[0], bb = s4[1];
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+            x[4] = bb.x; x[5] = bb.y; x[6] = bb.z; x[7] = bb.w;
+        } else if constexpr (DT == VSPEC_KV_F16) {
+            if (which) {
+                const uint16_t* vt = reinterpret_cast<const uint16_t*>(src) + tile * D * P + slot;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = half_bits_to_float(vt[(size_t)(8 * c + e) * P]);
+            } else {
+                unpack_f16x8(reinterpret_cast<const uint4*>(src + row * D * 2)[c], x);
+            }
+        } else {
+            const uint32_t w = reinterpret_cast<const uint32_t*>(src + row * (D / 2))[c];
+            const float sc = half_bits_to_float((which ? p.vs : p.ks)[row * (D / 32) + c / 4]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = nibble(w, e) * sc;
+        }
+        float4* d = reinterpret_cast<float4*>((which ? p.ov : p.ok) + ((size_t)i * p.hkv + h) * D) + 2 * c;
+        d[0] = make_float4(x[0], x[1], x[2], x[3]);
+        d[1] = make_float4(x[4], x[5], x[6], x[7]);
+    }
+}
+
 struct CompactParams {
     uint8_t* k;
     uint8_t* v;
@@ -655,7 +717,9 @@ size_t row_bytes_of(int32_t dtype, uint32_t d) {
     return dtype == VSPEC_KV_F32 ? (size_t)d * 4 : (dtype == VSPEC_KV_F16 ? (size_t)d * 2 : d / 2);
 }
 
-int check_kv(const VspecPagedKV* kv, const char* who) {
+// Geometry every kernel accepts; `decode` adds the attention kernels' limits
+// (head_dim 64 or 128, block_tokens a multiple of the 16-token tile).
+int check_kv(const VspecPagedKV* kv, const char* who, bool decode = false) {
     if (!kv) {
         set_err("%s: null pool", who);
         return 0;
@@ -664,15 +728,20 @@ int check_kv(const VspecPagedKV* kv, const char* who) {
         set_err("%s: bad dtype %d", who, (int)kv->dtype);
         return 0;
     }
-    if (kv->num_blocks == 0 || kv->num_kv_heads == 0) {
-        set_err("%s: empty pool", who);
+    if (kv->num_blocks == 0 || kv->num_kv_heads == 0 || kv->block_tokens == 0 || kv->head_dim == 0) {
+        set_err("%s: empty pool geometry", who);
         return 0;
     }
-    if (kv->block_tokens == 0 || kv->block_tokens % kTile != 0) {
+    const uint32_t quantum = kv->dtype == VSPEC_KV_INT4 ? 32u : 8u;
+    if (kv->head_dim % quantum != 0) {
+        set_err("%s: head_dim must be a multiple of %u", who, quantum);
+        return 0;
+    }
+    if (decode && kv->block_tokens % kTile != 0) {
         set_err("%s: block_tokens must be a positive multiple of %d", who, kTile);
         return 0;
     }
-    if (kv->head_dim != 64 && kv->head_dim != 128) {
+    if (decode && kv->head_dim != 64 && kv->head_dim != 128) {
         set_err("%s: head_dim must be 64 or 128", who);
         return 0;
     }
@@ -1002,9 +1071,46 @@ int vspec_rocm_kv_compact(const VspecPagedKV* kv, uint32_t n, const int32_t* src
     return 1;
 }
 
+int vspec_rocm_kv_gather_rows(const VspecPagedKV* kv, uint32_t n, const int32_t* pages,
+                              const int32_t* slots, float* out_k, float* out_v, void* stream) {
+    if (!check_kv(kv, "kv_gather_rows")) return 0;
+    if (n == 0) return 1;
+    if (!pages || !slots || !out_k || !out_v) {
+        set_err("kv_gather_rows: null argument");
+        return 0;
+    }
+    GatherRowsParams p;
+    p.k = (const uint8_t*)kv->k_data;
+    p.v = (const uint8_t*)kv->v_data;
+    p.ks = kv->k_scales;
+    p.vs = kv->v_scales;
+    p.pages = pages;
+    p.slots = slots;
+    p.ok = out_k;
+    p.ov = out_v;
+    p.n = n;
+    p.hkv = kv->num_kv_heads;
+    p.head_dim = kv->head_dim;
+    p.block_tokens = kv->block_tokens;
+    p.num_blocks = kv->num_blocks;
+    const uint64_t items = (uint64_t)n * kv->num_kv_heads * (kv->head_dim / 8) * 2;
+    uint64_t gx = (items + 255) / 256;
+    if (gx > 16384) gx = 16384;
+    hipStream_t s = (hipStream_t)stream;
+    if (kv->dtype == VSPEC_KV_F32) hipLaunchKernelGGL(kv_gather_rows<VSPEC_KV_F32>, dim3((unsigned)gx), dim3(256), 0, s, p);
+    else if (kv->dtype == VSPEC_KV_F16) hipLaunchKernelGGL(kv_gather_rows<VSPEC_KV_F16>, dim3((unsigned)gx), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(kv_gather_rows<VSPEC_KV_INT4>, dim3((unsigned)gx), dim3(256), 0, s, p);
+    HIP_CHECK(hipGetLastError(), "kv_gather_rows launch");
+    return 1;
+}
+
 size_t vspec_rocm_paged_decode_workspace_bytes(const VspecPagedAttnDesc* desc) {
     DecodePlan pl;
-    if (!desc || !plan_decode(desc, &pl)) return 0;
+    if (!desc) {
+        set_err("paged_decode_workspace_bytes: null descriptor");
+        return 0;
+    }
+    if (!check_kv(&desc->kv, "paged_decode_workspace_bytes", true) || !plan_decode(desc, &pl)) return 0;
     return pl.ws_bytes;
 }
 
@@ -1013,7 +1119,7 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
         set_err("paged_decode: null descriptor");
         return 0;
     }
-    if (!check_kv(&desc->kv, "paged_decode")) return 0;
+    if (!check_kv(&desc->kv, "paged_decode", true)) return 0;
     if (desc->batch == 0) return 1;
     if (!desc->block_tables || !desc->ctx_lens || !desc->q || !desc->out || desc->max_blocks_per_seq == 0) {
         set_err("paged_decode: null argument");

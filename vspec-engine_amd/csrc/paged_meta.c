@@ -1,0 +1,323 @@
+/*
+ * paged_meta.c -- host bookkeeping of the paged KV cache.
+ *
+ * Policy of the reference allocator, kv_paged_cache.c, with the caps lifted:
+ *   - sessions live in a fixed table of max_sessions slots, found by linear scan;
+ *   - pages are allocated first-fit (lowest free index); on exhaustion the
+ *     least-recently-touched session other than the requester is released whole and
+ *     the scan retried (:90-122);
+ *   - a page is freed when its reference count drops to zero (:37-59);
+ *   - prefix reuse shares whole source pages into an empty target while the
+ *     cumulative used count stays within max_tokens (:185-241); an append opens a
+ *     new page when the last page is full or shared (:268-290);
+ *   - a monotonically increasing clock stamps sessions and pages (:264-266).
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "vspec_rocm_paged.h"
+
+typedef struct Page {
+    uint8_t allocated;
+    uint32_t owner_slot;
+    uint32_t used_tokens;
+    uint32_t ref_count;
+    uint64_t last_touch_step;
+} Page;
+
+typedef struct Session {
+    uint8_t active;
+    uint64_t session_id;
+    uint64_t last_touch_step;
+    size_t total_tokens;
+    size_t page_count;
+    uint32_t* pages; /* max_pages_per_session entries */
+} Session;
+
+struct VspecRocmPagedMeta {
+    size_t page_tokens;
+    size_t max_pages;
+    size_t max_sessions;
+    size_t max_pages_per_session;
+    VspecRocmPagedStats stats;
+    Page* page;
+    Session* session;
+    uint32_t* page_lists;
+    uint64_t clock_step;
+};
+
+static int find_session(const VspecRocmPagedMeta* m, uint64_t id) {
+    if (!m || id == 0u) return -1;
+    for (size_t i = 0; i < m->max_sessions; ++i) {
+        if (m->session[i].active && m->session[i].session_id == id) return (int)i;
+    }
+    return -1;
+}
+
+static int find_free_session(const VspecRocmPagedMeta* m) {
+    for (size_t i = 0; i < m->max_sessions; ++i) {
+        if (!m->session[i].active) return (int)i;
+    }
+    return -1;
+}
+
+static void release_session(VspecRocmPagedMeta* m, int slot) {
+    Session* s = &m->session[slot];
+    for (size_t i = 0; i < s->page_count; ++i) {
+        const uint32_t p = s->pages[i];
+        if (p >= m->max_pages) continue;
+        if (m->page[p].ref_count > 0u) m->page[p].ref_count -= 1u;
+        if (m->page[p].ref_count == 0u) {
+            m->page[p].allocated = 0u;
+            m->page[p].owner_slot = 0u;
+            m->page[p].used_tokens = 0u;
+        }
+    }
+    uint32_t* keep = s->pages;
+    memset(s, 0, sizeof(*s));
+    s->pages = keep;
+}
+
+static int evict_lru(VspecRocmPagedMeta* m, int protect) {
+    int victim = -1;
+    uint64_t oldest = UINT64_MAX;
+    for (size_t i = 0; i < m->max_sessions; ++i) {
+        if (!m->session[i].active || (int)i == protect) continue;
+        if (m->session[i].last_touch_step < oldest) {
+            oldest = m->session[i].last_touch_step;
+            victim = (int)i;
+        }
+    }
+    if (victim < 0) return 0;
+    release_session(m, victim);
+    m->stats.evict_session_count += 1u;
+    return 1;
+}
+
+static long take_first_free(VspecRocmPagedMeta* m, int owner) {
+    for (size_t i = 0; i < m->max_pages; ++i) {
+        if (!m->page[i].allocated) {
+            Page* p = &m->page[i];
+            p->allocated = 1u;
+            p->owner_slot = (uint32_t)owner;
+            p->used_tokens = 0u;
+            p->ref_count = 1u;
+            p->last_touch_step = m->clock_step;
+            m->stats.page_alloc_count += 1u;
+            return (long)i;
+        }
+    }
+    return -1;
+}
+
+static long alloc_page(VspecRocmPagedMeta* m, int owner) {
+    long p = take_first_free(m, owner);
+    if (p >= 0) return p;
+    if (evict_lru(m, owner)) return take_first_free(m, owner);
+    return -1;
+}
+
+VspecRocmPagedMeta* vspec_rocm_paged_meta_create(size_t page_tokens, size_t max_pages,
+                                                 size_t max_sessions,
+                                                 size_t max_pages_per_session) {
+    if (page_tokens == 0u || max_pages == 0u || max_pages > UINT32_MAX) return NULL;
+    if (max_sessions == 0u) max_sessions = 128u;
+    if (max_pages_per_session == 0u) max_pages_per_session = 1024u;
+    VspecRocmPagedMeta* m = (VspecRocmPagedMeta*)calloc(1, sizeof(*m));
+    if (!m) return NULL;
+    m->page_tokens = page_tokens;
+    m->max_pages = max_pages;
+    m->max_sessions = max_sessions;
+    m->max_pages_per_session = max_pages_per_session;
+    m->page = (Page*)calloc(max_pages, sizeof(Page));
+    m->session = (Session*)calloc(max_sessions, sizeof(Session));
+    m->page_lists = (uint32_t*)calloc(max_sessions * max_pages_per_session, sizeof(uint32_t));
+    if (!m->page || !m->session || !m->page_lists) {
+        vspec_rocm_paged_meta_destroy(m);
+        return NULL;
+    }
+    vspec_rocm_paged_meta_reset(m);
+    return m;
+}
+
+void vspec_rocm_paged_meta_destroy(VspecRocmPagedMeta* m) {
+    if (!m) return;
+    free(m->page);
+    free(m->session);
+    free(m->page_lists);
+    free(m);
+}
+
+void vspec_rocm_paged_meta_reset(VspecRocmPagedMeta* m) {
+    if (!m) return;
+    memset(m->page, 0, m->max_pages * sizeof(Page));
+    memset(&m->stats, 0, sizeof(m->stats));
+    for (size_t i = 0; i < m->max_sessions; ++i) {
+        memset(&m->session[i], 0, sizeof(Session));
+        m->session[i].pages = m->page_lists + i * m->max_pages_per_session;
+    }
+    m->clock_step = 1u;
+}
+
+int vspec_rocm_paged_open_session(VspecRocmPagedMeta* m, uint64_t id) {
+    if (!m || id == 0u) return 0;
+    if (find_session(m, id) >= 0) return 1;
+    int slot = find_free_session(m);
+    if (slot < 0) {
+        if (!evict_lru(m, -1)) return 0;
+        slot = find_free_session(m);
+        if (slot < 0) return 0;
+    }
+    m->session[slot].active = 1u;
+    m->session[slot].session_id = id;
+    m->session[slot].last_touch_step = m->clock_step;
+    return 1;
+}
+
+int vspec_rocm_paged_close_session(VspecRocmPagedMeta* m, uint64_t id) {
+    const int slot = find_session(m, id);
+    if (slot < 0) return 0;
+    release_session(m, slot);
+    return 1;
+}
+
+int vspec_rocm_paged_reuse_prefix(VspecRocmPagedMeta* m, uint64_t target, uint64_t source,
+                                  size_t max_tokens) {
+    if (!m || target == 0u || source == 0u) return 0;
+    const int src = find_session(m, source);
+    if (src < 0) return 0;
+    if (!vspec_rocm_paged_open_session(m, target)) return 0;
+    const int dst = find_session(m, target);
+    if (dst < 0) return 0;
+    Session* t = &m->session[dst];
+    const Session* s = &m->session[src];
+    if (t->page_count != 0u) return 0;
+    size_t copied = 0;
+    for (size_t i = 0; i < s->page_count; ++i) {
+        if (t->page_count >= m->max_pages_per_session) break;
+        const uint32_t p = s->pages[i];
+        if (p >= m->max_pages) continue;
+        const size_t used = m->page[p].used_tokens;
+        if (max_tokens > 0u && copied >= max_tokens) break;
+        if (max_tokens > 0u && copied + used > max_tokens) break;
+        t->pages[t->page_count++] = p;
+        t->total_tokens += used;
+        m->page[p].ref_count += 1u;
+        copied += used;
+        m->stats.page_reuse_count += 1u;
+    }
+    t->last_touch_step = m->clock_step;
+    return 1;
+}
+
+int vspec_rocm_paged_reserve(VspecRocmPagedMeta* m, uint64_t id, uint32_t* page_out,
+                             uint32_t* slot_out) {
+    if (!m) return 0;
+    int slot = find_session(m, id);
+    if (slot < 0) {
+        if (!vspec_rocm_paged_open_session(m, id)) return 0;
+        slot = find_session(m, id);
+    }
+    if (slot < 0) return 0;
+    Session* s = &m->session[slot];
+    m->clock_step += 1u;
+    s->last_touch_step = m->clock_step;
+
+    long p = -1;
+    if (s->page_count > 0u) {
+        p = (long)s->pages[s->page_count - 1u];
+        if ((size_t)p >= m->max_pages) p = -1;
+    }
+    if (p >= 0 && (m->page[p].used_tokens >= m->page_tokens || m->page[p].ref_count > 1u)) p = -1;
+    if (p < 0) {
+        if (s->page_count >= m->max_pages_per_session) return 0;
+        p = alloc_page(m, slot);
+        if (p < 0) return 0;
+        s->pages[s->page_count++] = (uint32_t)p;
+    }
+    if (page_out) *page_out = (uint32_t)p;
+    if (slot_out) *slot_out = m->page[p].used_tokens;
+    m->page[p].used_tokens += 1u;
+    m->page[p].last_touch_step = m->clock_step;
+    s->total_tokens += 1u;
+    m->stats.append_token_count += 1u;
+    return 1;
+}
+
+int vspec_rocm_paged_locate(const VspecRocmPagedMeta* m, uint64_t id, size_t token_idx,
+                            uint32_t* page_out, uint32_t* slot_out) {
+    if (!m || !page_out || !slot_out) return 0;
+    const int slot = find_session(m, id);
+    if (slot < 0) return 0;
+    const Session* s = &m->session[slot];
+    if (token_idx >= s->total_tokens) return 0;
+    size_t remain = token_idx;
+    uint32_t page = 0u;  /* a walk that runs off the end lands on page 0, slot 0 (:333-334) */
+    size_t in_page = 0u;
+    for (size_t i = 0; i < s->page_count; ++i) {
+        const uint32_t p = s->pages[i];
+        if (p >= m->max_pages) return 0;
+        const size_t used = m->page[p].used_tokens;
+        if (remain < used) {
+            page = p;
+            in_page = remain;
+            break;
+        }
+        remain -= used;
+    }
+    *page_out = page;
+    *slot_out = (uint32_t)in_page;
+    return 1;
+}
+
+size_t vspec_rocm_paged_session_tokens(const VspecRocmPagedMeta* m, uint64_t id) {
+    const int slot = find_session(m, id);
+    return slot < 0 ? 0u : m->session[slot].total_tokens;
+}
+
+void vspec_rocm_paged_stats(const VspecRocmPagedMeta* m, VspecRocmPagedStats* out) {
+    if (!m || !out) return;
+    *out = m->stats;
+    out->free_pages = 0u;
+    out->active_sessions = 0u;
+    for (size_t i = 0; i < m->max_pages; ++i) {
+        if (!m->page[i].allocated) out->free_pages += 1u;
+    }
+    for (size_t i = 0; i < m->max_sessions; ++i) {
+        if (m->session[i].active) out->active_sessions += 1u;
+    }
+}
+
+size_t vspec_rocm_paged_session_pages(const VspecRocmPagedMeta* m, uint64_t id, uint32_t* out,
+                                      size_t cap) {
+    const int slot = find_session(m, id);
+    if (slot < 0) return 0u;
+    const Session* s = &m->session[slot];
+    for (size_t i = 0; out && i < s->page_count && i < cap; ++i) out[i] = s->pages[i];
+    return s->page_count;
+}
+
+int vspec_rocm_paged_page_info(const VspecRocmPagedMeta* m, size_t page, uint32_t* allocated,
+                               uint32_t* used_tokens, uint32_t* ref_count) {
+    if (!m || page >= m->max_pages) return 0;
+    if (allocated) *allocated = m->page[page].allocated;
+    if (used_tokens) *used_tokens = m->page[page].used_tokens;
+    if (ref_count) *ref_count = m->page[page].ref_count;
+    return 1;
+}
+
+int vspec_rocm_paged_block_table(const VspecRocmPagedMeta* m, uint64_t id, int32_t* out,
+                                 size_t cap, uint32_t* ctx_len) {
+    const int slot = find_session(m, id);
+    if (slot < 0 || !out) return 0;
+    const Session* s = &m->session[slot];
+    if (s->page_count > cap || s->total_tokens > (size_t)INT32_MAX) return 0;
+    for (size_t i = 0; i < s->page_count; ++i) {
+        const uint32_t p = s->pages[i];
+        if (p >= m->max_pages || p > (uint32_t)INT32_MAX) return 0;
+        if (i + 1u < s->page_count && m->page[p].used_tokens != m->page_tokens) return 0;
+        out[i] = (int32_t)p;
+    }
+    if (ctx_len) *ctx_len = (uint32_t)s->total_tokens;
+    return 1;
+}

@@ -113,7 +113,24 @@ class VspecKVCache(C.Structure):
     ]
 
 
-# Every symbol include/vspec_rocm.h declares, with its ctypes signature.
+class VspecRocmPagedStats(C.Structure):
+    """Same layout as the reference's VspecKVPagedStats (kv_paged_cache.h:11-18)."""
+
+    _fields_ = [
+        ("page_alloc_count", C.c_uint64),
+        ("page_reuse_count", C.c_uint64),
+        ("evict_session_count", C.c_uint64),
+        ("append_token_count", C.c_uint64),
+        ("free_pages", C.c_size_t),
+        ("active_sessions", C.c_size_t),
+    ]
+
+
+_u32p = C.POINTER(C.c_uint32)
+_i32p_ = C.POINTER(C.c_int32)
+_f32p = C.POINTER(C.c_float)
+
+# Every symbol include/*.h declares, with its ctypes signature.
 SIGNATURES = {
     "vspec_rocm_kv_pool_bytes": (C.c_size_t, [C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
     "vspec_rocm_kv_pool_create": (C.c_int, [C.POINTER(VspecPagedKV), C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
@@ -128,6 +145,29 @@ SIGNATURES = {
     "vspec_rocm_device_count": (C.c_int, []),
     "vspec_rocm_backend_available": (C.c_int, []),
     "vspec_make_rocm_backend": (VspecBackend, []),
+    # include/vspec_rocm_paged.h
+    "vspec_rocm_paged_meta_create": (_vp, [C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t]),
+    "vspec_rocm_paged_meta_destroy": (None, [_vp]),
+    "vspec_rocm_paged_meta_reset": (None, [_vp]),
+    "vspec_rocm_paged_open_session": (C.c_int, [_vp, C.c_uint64]),
+    "vspec_rocm_paged_close_session": (C.c_int, [_vp, C.c_uint64]),
+    "vspec_rocm_paged_reuse_prefix": (C.c_int, [_vp, C.c_uint64, C.c_uint64, C.c_size_t]),
+    "vspec_rocm_paged_reserve": (C.c_int, [_vp, C.c_uint64, _u32p, _u32p]),
+    "vspec_rocm_paged_locate": (C.c_int, [_vp, C.c_uint64, C.c_size_t, _u32p, _u32p]),
+    "vspec_rocm_paged_session_tokens": (C.c_size_t, [_vp, C.c_uint64]),
+    "vspec_rocm_paged_stats": (None, [_vp, C.POINTER(VspecRocmPagedStats)]),
+    "vspec_rocm_paged_session_pages": (C.c_size_t, [_vp, C.c_uint64, _u32p, C.c_size_t]),
+    "vspec_rocm_paged_page_info": (C.c_int, [_vp, C.c_size_t, _u32p, _u32p, _u32p]),
+    "vspec_rocm_paged_block_table": (C.c_int, [_vp, C.c_uint64, _i32p_, C.c_size_t, _u32p]),
+    "vspec_py_kv_cache_create": (C.c_int, [C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t]),
+    "vspec_py_kv_cache_destroy": (None, [C.c_int]),
+    "vspec_py_kv_cache_reset": (C.c_int, [C.c_int]),
+    "vspec_py_kv_cache_append": (C.c_int, [C.c_int, C.c_uint64, _f32p, _f32p]),
+    "vspec_py_kv_cache_session_tokens": (C.c_size_t, [C.c_int, C.c_uint64]),
+    "vspec_py_kv_cache_read": (C.c_size_t, [C.c_int, C.c_uint64, _f32p, _f32p, C.c_size_t]),
+    "vspec_py_kv_cache_meta": (_vp, [C.c_int]),
+    "vspec_py_kv_cache_pool": (C.POINTER(VspecPagedKV), [C.c_int]),
+    "vspec_rocm_kv_gather_rows": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, _vp, _vp]),
 }
 
 _LIB = None

@@ -1,0 +1,136 @@
+"""Session-level paged KV cache over the GPU-resident handle API.
+
+`CorePagedKVCache` keeps the method names, argument meaning and return conventions of
+the reference's Python wrapper (Vspec-chat/python/runtime_core_bridge.py:479-549):
+append one token's [H][D] keys/values, count a session's tokens, read them back as
+[T][H][D] float32 arrays.  The token data lives in HBM and moves through the library's
+append and row-gather kernels; page placement follows the reference allocator.  Unlike
+the reference wrapper, a missing library raises instead of reporting `available=False`:
+this package has no CPU path to fall back to.
+
+The extra methods (`reuse_prefix`, `block_table`, `stats`, `device_pool`) expose what a
+batched GPU decode step needs from the same cache.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import VspecPagedKV, VspecRocmError, VspecRocmPagedStats, last_error, lib
+
+_f32p = C.POINTER(C.c_float)
+
+
+class HandlePool:
+    """A handle's device pool in the shape `paged_decode` expects (`desc()`)."""
+
+    def __init__(self, kv: VspecPagedKV):
+        self._kv = kv
+        self.dtype, self.num_blocks, self.block_tokens = kv.dtype, kv.num_blocks, kv.block_tokens
+        self.num_kv_heads, self.head_dim = kv.num_kv_heads, kv.head_dim
+
+    def desc(self) -> VspecPagedKV:
+        return self._kv
+
+
+class CorePagedKVCache:
+    def __init__(self, page_tokens: int, max_pages: int, num_heads: int, head_dim: int, session_id: int = 1) -> None:
+        L = lib()
+        self.handle = int(L.vspec_py_kv_cache_create(page_tokens, max_pages, num_heads, head_dim))
+        if self.handle <= 0:
+            raise VspecRocmError(f"vspec_py_kv_cache_create failed: {last_error()}")
+        self.session_id = int(session_id)
+        self.num_heads = int(num_heads)
+        self.head_dim = int(head_dim)
+        self.page_tokens = int(page_tokens)
+
+    @property
+    def available(self) -> bool:
+        return self.handle > 0
+
+    def reset(self) -> None:
+        if self.available:
+            lib().vspec_py_kv_cache_reset(self.handle)
+
+    def append(self, key_token, value_token, session_id: int | None = None) -> bool:
+        if not self.available:
+            return False
+        k = np.ascontiguousarray(key_token, dtype=np.float32).reshape(-1)
+        v = np.ascontiguousarray(value_token, dtype=np.float32).reshape(-1)
+        if k.size != self.num_heads * self.head_dim or v.size != k.size:
+            raise ValueError(f"append expects {self.num_heads}x{self.head_dim} floats per token")
+        sid = self.session_id if session_id is None else int(session_id)
+        return bool(lib().vspec_py_kv_cache_append(self.handle, sid, k.ctypes.data_as(_f32p),
+                                                   v.ctypes.data_as(_f32p)))
+
+    def session_tokens(self, session_id: int | None = None) -> int:
+        if not self.available:
+            return 0
+        sid = self.session_id if session_id is None else int(session_id)
+        return int(lib().vspec_py_kv_cache_session_tokens(self.handle, sid))
+
+    def read_tokens(self, max_tokens: int | None = None, session_id: int | None = None):
+        if not self.available:
+            return None, None
+        sid = self.session_id if session_id is None else int(session_id)
+        n = self.session_tokens(sid)
+        if max_tokens is not None:
+            n = min(n, int(max_tokens))
+        shape = (self.num_heads, self.head_dim)
+        if n <= 0:
+            empty = np.empty((0, *shape), np.float32)
+            return empty, empty.copy()
+        keys = np.empty((n, *shape), np.float32)
+        values = np.empty((n, *shape), np.float32)
+        got = int(lib().vspec_py_kv_cache_read(self.handle, sid, keys.ctypes.data_as(_f32p),
+                                               values.ctypes.data_as(_f32p), n))
+        if got <= 0:
+            return None, None
+        return keys[:got], values[:got]
+
+    # ---- beyond the reference wrapper: the allocator and the device pool ----
+    def _meta(self):
+        return lib().vspec_py_kv_cache_meta(self.handle)
+
+    def open_session(self, session_id: int) -> bool:
+        return bool(lib().vspec_rocm_paged_open_session(self._meta(), int(session_id)))
+
+    def close_session(self, session_id: int) -> bool:
+        return bool(lib().vspec_rocm_paged_close_session(self._meta(), int(session_id)))
+
+    def reuse_prefix(self, target_session: int, source_session: int, max_tokens: int) -> bool:
+        return bool(lib().vspec_rocm_paged_reuse_prefix(self._meta(), int(target_session), int(source_session),
+                                                         int(max_tokens)))
+
+    def stats(self) -> dict:
+        st = VspecRocmPagedStats()
+        lib().vspec_rocm_paged_stats(self._meta(), C.byref(st))
+        return {name: getattr(st, name) for name, _ in st._fields_}
+
+    def block_table(self, session_id: int, max_blocks: int):
+        """(int32 [max_blocks] table padded with -1, context length) or None when a
+        shared, partly filled page sits in the middle of the session."""
+        tab = np.full(max_blocks, -1, np.int32)
+        ctx = C.c_uint32()
+        ok = lib().vspec_rocm_paged_block_table(self._meta(), int(session_id),
+                                                tab.ctypes.data_as(C.POINTER(C.c_int32)), max_blocks,
+                                                C.byref(ctx))
+        return (tab, int(ctx.value)) if ok else None
+
+    def device_pool(self) -> HandlePool:
+        p = lib().vspec_py_kv_cache_pool(self.handle)
+        if not p:
+            raise VspecRocmError("handle has no device pool")
+        return HandlePool(p.contents)
+
+    def close(self) -> None:
+        if self.handle > 0:
+            lib().vspec_py_kv_cache_destroy(self.handle)
+            self.handle = 0
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
