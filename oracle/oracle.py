@@ -124,6 +124,8 @@ class Oracle:
             "vo_paged_compact": (C.c_int, [C.POINTER(VoPagedKV), C.c_uint32, _i32p, _i32p]),
             "vo_paged_decode_attention": (C.c_int, [C.c_int, _sz, C.POINTER(VoPagedKV), C.c_uint32, C.c_uint32, _i32p, C.c_uint32, _i32p, _f32p, _f32p]),
             "vo_attention_textbook_f64": (None, [_f32p, _f32p, _sz, _f32p, _sz, _sz, _sz, C.POINTER(C.c_double)]),
+            "vo_int4_ks_index": (_sz, [C.POINTER(VoPagedKV), _sz, _sz, _sz, _sz]),
+            "vo_int4_v_byte": (_sz, [C.POINTER(VoPagedKV), _sz, _sz, _sz, _sz, C.POINTER(C.c_int)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

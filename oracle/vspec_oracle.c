@@ -590,7 +590,8 @@ static int vo_kv_valid(const VoPagedKV* kv) {
         kv->num_kv_heads == 0u || kv->head_dim == 0u || kv->dtype < 0 || kv->dtype > 2) {
         return 0;
     }
-    if (kv->dtype == 2 && (kv->head_dim % 32u != 0u || !kv->k_scales || !kv->v_scales)) {
+    if (kv->dtype == 2 && (kv->head_dim % 32u != 0u || kv->head_dim > 1024u ||
+                           kv->block_tokens % 16u != 0u || !kv->k_scales || !kv->v_scales)) {
         return 0;
     }
     return 1;
@@ -607,8 +608,68 @@ static long vo_phys_block(const VoPagedKV* kv, const int32_t* block_tables, uint
 }
 
 /* f16 V tiles are d-major: element (d, slot) of tile (b, h) at ((b*H + h)*D + d)*P + slot.
+ * int4 pools (block_tokens a multiple of 16):
+ *   K codes: token-major rows of D/2 bytes, element e in nibble e%2 of byte e/2;
+ *   K scales: group-major, scale (group c, slot) at ((b*H + h)*G + c)*P + slot;
+ *   V codes: 16-token tiles of 8*D bytes; element d of the token at tile position
+ *            t = 4*g + r sits in byte (g*16 + d%16)*(D/8) + 4*(d/32) + 2*(r&1) + (r>>1)
+ *            of its tile, low nibble when (d/16) is even, high nibble otherwise;
+ *   V scales: token-major rows of G scales.
  * Every other array is token-major (row index (b*H + h)*P + slot). */
 static int vo_v_dmajor(const VoPagedKV* kv, int is_v) { return is_v && kv->dtype == 1; }
+
+size_t vo_int4_ks_index(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t group) {
+    const size_t G = kv->head_dim / 32u;
+    return ((b * kv->num_kv_heads + h) * G + group) * kv->block_tokens + slot;
+}
+
+size_t vo_int4_v_byte(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t d, int* high) {
+    const size_t D = kv->head_dim, P = kv->block_tokens;
+    const size_t t = slot % 16u, g = t / 4u, r = t % 4u;
+    *high = (int)((d / 16u) & 1u);
+    return (b * kv->num_kv_heads + h) * (P * D / 2u) + (slot / 16u) * (8u * D) +
+           (g * 16u + d % 16u) * (D / 8u) + 4u * (d / 32u) + 2u * (r & 1u) + (r >> 1);
+}
+
+/* Canonical packed row (D/2 bytes, element e in nibble e%2 of byte e/2) <-> pool. */
+static void vo_int4_put_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
+                            const uint8_t* codes, const uint16_t* sc) {
+    const size_t D = kv->head_dim, G = D / 32u;
+    const size_t row = vo_row_index(kv, b, h, slot);
+    if (!is_v) {
+        memcpy((uint8_t*)kv->k_data + row * (D / 2u), codes, D / 2u);
+        for (size_t c = 0; c < G; ++c) kv->k_scales[vo_int4_ks_index(kv, b, h, slot, c)] = sc[c];
+        return;
+    }
+    uint8_t* v = (uint8_t*)kv->v_data;
+    for (size_t d = 0; d < D; ++d) {
+        int high = 0;
+        const size_t at = vo_int4_v_byte(kv, b, h, slot, d, &high);
+        const uint8_t nib = (uint8_t)((codes[d / 2u] >> (4u * (d % 2u))) & 0xfu);
+        v[at] = high ? (uint8_t)((v[at] & 0x0fu) | (nib << 4)) : (uint8_t)((v[at] & 0xf0u) | nib);
+    }
+    memcpy(kv->v_scales + row * G, sc, G * 2u);
+}
+
+static void vo_int4_get_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
+                            uint8_t* codes, uint16_t* sc) {
+    const size_t D = kv->head_dim, G = D / 32u;
+    const size_t row = vo_row_index(kv, b, h, slot);
+    if (!is_v) {
+        memcpy(codes, (const uint8_t*)kv->k_data + row * (D / 2u), D / 2u);
+        for (size_t c = 0; c < G; ++c) sc[c] = kv->k_scales[vo_int4_ks_index(kv, b, h, slot, c)];
+        return;
+    }
+    const uint8_t* v = (const uint8_t*)kv->v_data;
+    memset(codes, 0, D / 2u);
+    for (size_t d = 0; d < D; ++d) {
+        int high = 0;
+        const size_t at = vo_int4_v_byte(kv, b, h, slot, d, &high);
+        const uint8_t nib = (uint8_t)(high ? (v[at] >> 4) : (v[at] & 0xfu));
+        codes[d / 2u] |= (uint8_t)(nib << (4u * (d % 2u)));
+    }
+    memcpy(sc, kv->v_scales + row * G, G * 2u);
+}
 
 /* Write one token-head row (D elements) from fp32 values into the pool. */
 static void vo_store_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
@@ -625,7 +686,12 @@ static void vo_store_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size
     } else if (kv->dtype == 1) {
         vo_f32_to_f16(src, (uint16_t*)data + row * D, D);
     } else {
-        vo_int4_quantize_head(src, D, (uint8_t*)data + row * (D / 2u), scales + row * (D / 32u));
+        uint8_t codes[512];
+        uint16_t sc[32];
+        (void)data;
+        (void)scales;
+        vo_int4_quantize_head(src, D, codes, sc);
+        vo_int4_put_row(kv, is_v, b, h, slot, codes, sc);
     }
 }
 
@@ -644,8 +710,12 @@ static void vo_load_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_
     } else if (kv->dtype == 1) {
         vo_f16_to_f32((const uint16_t*)data + row * D, dst, D);
     } else {
-        vo_int4_dequantize_head((const uint8_t*)data + row * (D / 2u), scales + row * (D / 32u), D,
-                                dst);
+        uint8_t codes[512];
+        uint16_t sc[32];
+        (void)data;
+        (void)scales;
+        vo_int4_get_row(kv, is_v, b, h, slot, codes, sc);
+        vo_int4_dequantize_head(codes, sc, D, dst);
     }
 }
 
@@ -664,8 +734,10 @@ static void vo_copy_row_raw(const VoPagedKV* kv, int is_v, size_t b, size_t h, s
     } else if (kv->dtype == 1) {
         memcpy(out_row, (const uint16_t*)data + row * D, D * 2u);
     } else {
-        memcpy(out_row, (const uint8_t*)data + row * (D / 2u), D / 2u);
-        memcpy(out_scales, scales + row * G, G * 2u);
+        (void)data;
+        (void)scales;
+        (void)G;
+        vo_int4_get_row(kv, is_v, b, h, slot, (uint8_t*)out_row, out_scales);
     }
 }
 

@@ -107,6 +107,13 @@ typedef struct VoPagedKV {
     uint16_t* v_scales;
 } VoPagedKV;
 
+/* int4 pool addressing (block_tokens a multiple of 16): index of the K scale of
+ * (block b, head h, slot, group) in k_scales, and byte offset of V element (slot, d)
+ * in v_data (*high: 1 when it is the byte's high nibble).  K codes and V scales are
+ * token-major rows. */
+size_t vo_int4_ks_index(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t group);
+size_t vo_int4_v_byte(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t d, int* high);
+
 /* Append n_new tokens per sequence at logical positions start_pos[b] .. +n_new-1.
  * k_new/v_new: [B][n_new][H][D] in src_dtype (0 f32, 1 f16).  Returns 1/0. */
 int vo_paged_append(const VoPagedKV* kv, uint32_t batch, const int32_t* block_tables,

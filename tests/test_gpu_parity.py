@@ -243,11 +243,13 @@ def test_decode_edges(oracle, gpu, dtype, D, Hq, Hkv):
             check_attention(oracle, case, got, mode, subset=range(len(ctx) - 1))
 
 
-def test_decode_outliers_fire_clamp(oracle, gpu):
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+def test_decode_outliers_fire_clamp(oracle, gpu, dtype):
     """Large outliers make the std-clamp (and in mode R the +-16 clip and +-24 logit
-    clip) change the result; the GPU must follow the reference there too."""
-    say("[outliers]")
-    case = make_case(oracle, DTYPE_F32, 2, 8, 2, 128, 16, [300, 77], seed=91)
+    clip) change the result; the GPU must follow the reference there too (the f16 and
+    int4 kernels take their exact-score path for these keys)."""
+    say(f"[outliers] dtype={dtype}")
+    case = make_case(oracle, dtype, 2, 8, 2, 128, 16, [300, 77], seed=91, src16=False)
     k = case.k_tokens.copy()
     k[0, ::7, 0, 3] = 40.0
     k[1, ::5, 1, 100] = -25.0

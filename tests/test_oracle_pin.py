@@ -319,6 +319,42 @@ def test_paged_append_gather_roundtrip(oracle, dtype):
                     assert np.array_equal(fk[r, h], oracle.int4_dequantize_head(c, s, D))
 
 
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_int4_pool_layout_is_a_bijection(oracle, D):
+    """Every (block, head, slot, element) of an int4 pool owns exactly one V nibble and
+    every (block, head, slot, group) one K scale, inside the pool; a V byte holds the
+    two d-tiles of ONE token, so appends of different tokens never share a byte."""
+    nb, P, H = 3, 32, 2
+    pool = HostPool(DTYPE_INT4, nb, P, H, D)
+    desc = pool.desc()
+    hi = C.c_int()
+    seen = np.zeros((pool.v.size, 2), np.int64) - 1
+    for b in range(nb):
+        for h in range(H):
+            for slot in range(P):
+                for d in range(D):
+                    at = oracle.lib.vo_int4_v_byte(C.byref(desc), b, h, slot, d, C.byref(hi))
+                    assert at < pool.v.size and seen[at, hi.value] < 0
+                    seen[at, hi.value] = ((b * H + h) * P + slot)
+    assert (seen >= 0).all()
+    assert (seen[:, 0] == seen[:, 1]).all()  # one token per byte
+    G = D // 32
+    idx = sorted(oracle.lib.vo_int4_ks_index(C.byref(desc), b, h, s, c)
+                 for b in range(nb) for h in range(H) for s in range(P) for c in range(G))
+    assert idx == list(range(pool.ks.size))
+    # the low nibble of a byte is an even 16-wide d-tile, the high nibble the next one
+    at0 = oracle.lib.vo_int4_v_byte(C.byref(desc), 1, 1, 21, 5, C.byref(hi))
+    assert hi.value == 0
+    at1 = oracle.lib.vo_int4_v_byte(C.byref(desc), 1, 1, 21, 21, C.byref(hi))
+    assert hi.value == 1 and at1 == at0
+
+
+def test_int4_pool_needs_whole_tiles(oracle):
+    pool = HostPool(DTYPE_INT4, 2, 24, 1, 64)
+    x = np.zeros((1, 1, 1, 64), np.float32)
+    assert not oracle.paged_append(pool, np.array([[0, 1]], np.int32), np.zeros(1, np.int32), x, x)
+
+
 def test_paged_gather_equals_reference_read(oracle, ref):
     """The reference pool (token-major pages, capi.c gather) and the build's layout
     hold the same tokens when the block table equals the reference session's pages."""

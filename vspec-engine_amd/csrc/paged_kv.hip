@@ -55,19 +55,18 @@ struct Row {
     static constexpr int kScales = DT == VSPEC_KV_INT4 ? D / 32 : 0;
 };
 
-// K-side layout: LPK lanes hold one key, 16 elements per lane.
+// K-side layout of the VALU decode kernel (f32 and f16 pools): LPK lanes hold one
+// key, 16 elements per lane.
 //   f16:  chunks of 8 elements (16 B), lane chunks sub, sub+LPK
 //   f32:  chunks of 4 elements (16 B), lane chunks sub + j*LPK, j < 4
-//   int4: 16 consecutive elements (8 B of codes), one scale
 template <int DT, int D>
 __device__ __forceinline__ int k_elem(int sub, int e) {
+    static_assert(DT != VSPEC_KV_INT4, "int4 pools decode on the matrix cores");
     constexpr int LPK = D / 16;
     if constexpr (DT == VSPEC_KV_F16) {
         return 8 * (sub + (e / 8) * LPK) + (e % 8);
-    } else if constexpr (DT == VSPEC_KV_F32) {
-        return 4 * (sub + (e / 4) * LPK) + (e % 4);
     } else {
-        return 16 * sub + e;
+        return 4 * (sub + (e / 4) * LPK) + (e % 4);
     }
 }
 
@@ -78,7 +77,7 @@ __device__ __forceinline__ void load_k16(const DecodeParams& p, size_t row, int 
         const uint4* src = reinterpret_cast<const uint4*>(p.k + row * (size_t)(D * 2));
         unpack_f16x8(src[sub], x);
         unpack_f16x8(src[sub + LPK], x + 8);
-    } else if constexpr (DT == VSPEC_KV_F32) {
+    } else {
         const float4* src = reinterpret_cast<const float4*>(p.k + row * (size_t)(D * 4));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -88,34 +87,22 @@ __device__ __forceinline__ void load_k16(const DecodeParams& p, size_t row, int 
             x[4 * j + 2] = w.z;
             x[4 * j + 3] = w.w;
         }
-    } else {
-        const uint2 w = reinterpret_cast<const uint2*>(p.k + row * (size_t)(D / 2))[sub];
-        const float sc = half_bits_to_float(p.ks[row * (size_t)(D / 32) + sub / 2]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x[i] = nibble(w.x, i) * sc;
-            x[8 + i] = nibble(w.y, i) * sc;
-        }
     }
 }
 
-// V-side layout: D/8 lanes per token, lane chunk c holds elements 8c..8c+7.
+// V-side layout of the VALU decode kernel: D/8 lanes per token, lane chunk c holds
+// elements 8c..8c+7 (f16 V tiles are d-major, f32 token-major).
 template <int DT, int D>
 __device__ __forceinline__ void load_v8(const DecodeParams& p, size_t row, int c, float* x) {
     if constexpr (DT == VSPEC_KV_F16) {
         const uint4 w = reinterpret_cast<const uint4*>(p.v + row * (size_t)(D * 2))[c];
         unpack_f16x8(w, x);
-    } else if constexpr (DT == VSPEC_KV_F32) {
+    } else {
         const float4* src = reinterpret_cast<const float4*>(p.v + row * (size_t)(D * 4));
         const float4 a = src[2 * c];
         const float4 b = src[2 * c + 1];
         x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
         x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-    } else {
-        const uint32_t w = reinterpret_cast<const uint32_t*>(p.v + row * (size_t)(D / 2))[c];
-        const float sc = half_bits_to_float(p.vs[row * (size_t)(D / 32) + c / 4]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = nibble(w, i) * sc;
     }
 }
 
@@ -485,10 +472,26 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
                 const int code = rr > 7.0f ? 7 : (rr >= -8.0f ? (int)rr : -8);
                 w[e / 8] |= ((uint32_t)code & 0xfu) << (4 * (e % 8));
             }
-            uint4* d4 = reinterpret_cast<uint4*>(dst + row * (p.head_dim / 2) + e0 / 2);
-            *d4 = make_uint4(w[0], w[1], w[2], w[3]);
-            uint16_t* sd = which ? p.vs : p.ks;
-            sd[row * (p.head_dim / 32) + c] = (uint16_t)s16;
+            const size_t bh = (size_t)phys * p.hkv + h;
+            if (which) {
+                // V tiles: byte n of this group's 16 holds d = 32c + n (low nibble) and
+                // d = 32c + 16 + n (high nibble) of this token, at lane chunk (g, n)
+                const uint32_t tt = slot & 15u, tg = tt >> 2, tr = tt & 3u;
+                uint8_t* vb = dst + bh * ((size_t)p.block_tokens * p.head_dim / 2) +
+                              (size_t)(slot >> 4) * (8u * p.head_dim) + (size_t)(16u * tg) * (p.head_dim / 8u) +
+                              4u * c + 2u * (tr & 1u) + (tr >> 1);
+#pragma unroll
+                for (int nn = 0; nn < 16; ++nn) {
+                    const uint32_t lo = (w[nn / 8] >> (4 * (nn % 8))) & 0xfu;
+                    const uint32_t hi = (w[2 + nn / 8] >> (4 * (nn % 8))) & 0xfu;
+                    vb[(size_t)nn * (p.head_dim / 8u)] = (uint8_t)(lo | (hi << 4));
+                }
+                p.vs[row * (p.head_dim / 32) + c] = (uint16_t)s16;
+            } else {
+                uint4* d4 = reinterpret_cast<uint4*>(dst + row * (p.head_dim / 2) + e0 / 2);
+                *d4 = make_uint4(w[0], w[1], w[2], w[3]);
+                p.ks[int4_ks_index(bh, p.head_dim / 32, p.block_tokens, slot, c)] = (uint16_t)s16;
+            }
         }
     }
 }
@@ -574,9 +577,12 @@ __global__ __launch_bounds__(256) void kv_gather(GatherParams p) {
             } else if constexpr (DT == VSPEC_KV_F16) {
                 unpack_f16x8(reinterpret_cast<const uint4*>(src + row * row_bytes)[c], x);
             } else {
-                const uint32_t w = reinterpret_cast<const uint32_t*>(src + row * row_bytes)[c];
-                const uint16_t* sc = which ? p.vs : p.ks;
-                const float s = half_bits_to_float(sc[row * (D / 32) + c / 4]);
+                const size_t bh = (size_t)phys * p.hkv + h;
+                const uint32_t slot = t % p.block_tokens;
+                const uint32_t w = which ? int4_v_canonical_dword(src, bh, p.block_tokens, D, slot, c)
+                                         : reinterpret_cast<const uint32_t*>(src + row * row_bytes)[c];
+                const float s = half_bits_to_float(
+                    which ? p.vs[row * (D / 32) + c / 4] : p.ks[int4_ks_index(bh, D / 32, p.block_tokens, slot, c / 4)]);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) x[i] = nibble(w, i) * s;
             }
@@ -584,12 +590,16 @@ __global__ __launch_bounds__(256) void kv_gather(GatherParams p) {
             d[0] = make_float4(x[0], x[1], x[2], x[3]);
             d[1] = make_float4(x[4], x[5], x[6], x[7]);
         } else if constexpr (DT == VSPEC_KV_INT4) {
+            // output rows are canonical packed codes whatever the pool layout
+            const size_t bh = (size_t)phys * p.hkv + h;
+            const uint32_t slot = t % p.block_tokens;
             reinterpret_cast<uint32_t*>(dst + orow * row_bytes)[c] =
-                reinterpret_cast<const uint32_t*>(src + row * row_bytes)[c];
+                which ? int4_v_canonical_dword(src, bh, p.block_tokens, D, slot, c)
+                      : reinterpret_cast<const uint32_t*>(src + row * row_bytes)[c];
             if (c < D / 32) {
-                const uint16_t* sc = which ? p.vs : p.ks;
                 uint16_t* od = which ? p.ovs : p.oks;
-                od[orow * (D / 32) + c] = sc[row * (D / 32) + c];
+                od[orow * (D / 32) + c] =
+                    which ? p.vs[row * (D / 32) + c] : p.ks[int4_ks_index(bh, D / 32, p.block_tokens, slot, c)];
             }
         } else {
             reinterpret_cast<uint4*>(dst + orow * row_bytes)[c] =
@@ -649,8 +659,10 @@ __global__ __launch_bounds__(256) void kv_gather_rows(GatherRowsParams p) {
                 unpack_f16x8(reinterpret_cast<const uint4*>(src + row * D * 2)[c], x);
             }
         } else {
-            const uint32_t w = reinterpret_cast<const uint32_t*>(src + row * (D / 2))[c];
-            const float sc = half_bits_to_float((which ? p.vs : p.ks)[row * (D / 32) + c / 4]);
+            const uint32_t w = which ? int4_v_canonical_dword(src, tile, P, D, slot, c)
+                                     : reinterpret_cast<const uint32_t*>(src + row * (D / 2))[c];
+            const float sc = half_bits_to_float(which ? p.vs[row * (D / 32) + c / 4]
+                                                      : p.ks[int4_ks_index(tile, D / 32, P, slot, c / 4)]);
 #pragma unroll
             for (int e = 0; e < 8; ++e) x[e] = nibble(w, e) * sc;
         }
@@ -735,6 +747,10 @@ int check_kv(const VspecPagedKV* kv, const char* who, bool decode = false) {
     const uint32_t quantum = kv->dtype == VSPEC_KV_INT4 ? 32u : 8u;
     if (kv->head_dim % quantum != 0) {
         set_err("%s: head_dim must be a multiple of %u", who, quantum);
+        return 0;
+    }
+    if (kv->dtype == VSPEC_KV_INT4 && kv->block_tokens % kTile != 0) {
+        set_err("%s: int4 pools need block_tokens a multiple of %d", who, kTile);
         return 0;
     }
     if (decode && kv->block_tokens % kTile != 0) {
@@ -1186,7 +1202,7 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
     switch (desc->kv.dtype) {
         case VSPEC_KV_F32: ok = dispatch_d<VSPEC_KV_F32>(D, pl.gw, p, grid, s); break;
         case VSPEC_KV_F16: ok = launch_decode_mfma_f16(p, D, pl.gw, grid, s); break;
-        default: ok = dispatch_d<VSPEC_KV_INT4>(D, pl.gw, p, grid, s); break;
+        default: ok = launch_decode_mfma_int4(p, D, pl.gw, grid, s); break;
     }
     if (!ok) {
         set_err("paged_decode: no kernel for head_dim %u, group %u", D, pl.gw);
