@@ -5,9 +5,9 @@
 // Per wave and 16-token tile of one kv head:
 //   S^T[16 tok][16 col] = K[16 tok][D] x Q'^T      v_mfma_f32_16x16x32_f16, A = K rows as
 //                                                   loaded, B = q' split in fp16 hi + lo
-//                                                   (two MFMAs per 32-wide d chunk)
+//                                                   (separate accumulator chains)
 //   O^T[d][16 col]     += V^T[d][16 tok] x P^T     v_mfma_f32_16x16x16f16, A = V^T rows
-//                                                   (V is stored d-major per tile), B = p
+//                                                   (V is stored d-major per block), B = p
 //                                                   hi + lo taken straight from the S^T
 //                                                   accumulator registers
 // Columns 0..GW-1 are the GQA query heads that share the tile; the rest stay zero.
@@ -26,7 +26,6 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ h8_t as_h8(uint4 w) { return __builtin_bit_cast(h8_t, w); }
-__device__ __forceinline__ h4_t as_h4(uint2 w) { return __builtin_bit_cast(h4_t, w); }
 __device__ __forceinline__ h2_t as_h2(uint32_t w) { return __builtin_bit_cast(h2_t, w); }
 
 template <int D>
@@ -35,8 +34,9 @@ struct Frags {
     uint2 v[D / 16];  // V^T row d = 16j + n, slots 4g .. 4g+3 of the tile
 };
 
-// PB: block_tokens known at compile time (16), or 0 for any multiple of 16
-template <int D, int GW, int PB>
+// PB: block_tokens known at compile time (16), or 0 for any multiple of 16;
+// NB: tiles in flight per wave
+template <int D, int GW, int PB, int NB>
 __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     constexpr int NQK = D / 32;  // QK MFMAs per tile (each on 32 d)
     constexpr int NDT = D / 16;  // PV d-tiles
@@ -114,10 +114,15 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const _Float16* kbase = reinterpret_cast<const _Float16*>(p.k);
     const _Float16* vbase = reinterpret_cast<const _Float16*>(p.v);
 
+    // Loads are issued unconditionally (a tile past the range or behind an invalid
+    // table entry reads block 0 and reports false): with no branches around them the
+    // compiler counts outstanding loads exactly and waits only for the tile it needs.
     auto load = [&](int tile, Frags<D>& f) -> bool {
-        const int phys = table[tile / tiles_per_block];
-        if (phys < 0 || (uint32_t)phys >= p.num_blocks) return false;
-        const size_t tidx = (size_t)phys * p.hkv + hk;
+        tile = __builtin_amdgcn_readfirstlane(tile);
+        const bool in_range = tile < tile_end;
+        const int entry = table[(in_range ? tile : tile_end - 1) / tiles_per_block];
+        const bool ok = in_range && entry >= 0 && (uint32_t)entry < p.num_blocks;
+        const size_t tidx = (size_t)(ok ? entry : 0) * p.hkv + hk;
         const int slot0 = (tile % tiles_per_block) * kTile;
         const uint4* kr = reinterpret_cast<const uint4*>(kbase + (tidx * P + slot0 + n) * D + 8 * g);
 #pragma unroll
@@ -125,22 +130,30 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         const _Float16* vt = vbase + tidx * (size_t)D * P + slot0 + 4 * g;
 #pragma unroll
         for (int j = 0; j < NDT; ++j) f.v[j] = *reinterpret_cast<const uint2*>(vt + (size_t)(16 * j + n) * P);
-        return true;
+        return ok;
     };
 
     f4_t acc[NDT];
 #pragma unroll
     for (int j = 0; j < NDT; ++j) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY;  // running max of head n (log2 units), per lane
-    float l_run = 0.f;        // running sum of p for head n over this lane's tokens
+    // running max starts finite so exp2(s - m_run) is 0, never NaN, in the columns
+    // that hold no head (their scores stay -inf)
+    float m_run = -1e30f;
+    float l_run = 0.f;  // sum of p for head n over this lane's tokens
+    // score clip per lane: columns that hold no head clip to -inf (3-bit mode: +-24*log2e)
+    const float clip_hi = n < GW ? p.logit_clip : -INFINITY;
+    const float clip_lo = n < GW ? -p.logit_clip : -INFINITY;
     const h2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-    // one 16-token tile: clamp screen, scores, online softmax, P.V
-    auto process = [&](Frags<D>& f, const int tile) {
-        const int tok0 = tile * kTile;
-        const int nvalid = min(kTile, ctx - tok0);
-
-        // ---- clamp screen for key n (this lane holds 8*NQK of its elements) ----
+    // Clamp screen of key n (this lane holds 8*NQK of its elements): mean and E[x^2]
+    // from v_dot2 sums over the whole key, max|x| over this lane's part.  `flag` is set
+    // in a lane whose part may reach the clamp threshold; key n is flagged when any of
+    // its four lanes is (tokens() folds the wave's ballot).
+    struct Screen {
+        float mean;
+        bool flag;
+    };
+    auto screen = [&](const Frags<D>& f, const int nvalid) -> Screen {
         float s1 = 0.f, s2 = 0.f;
         h2_t mx2 = {(_Float16)0.f, (_Float16)0.f};
 #pragma unroll
@@ -154,119 +167,84 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
                 mx2 = __builtin_elementwise_max(mx2, __builtin_elementwise_abs(kv2));
             }
         }
-        float mx = fmaxf((float)mx2[0], (float)mx2[1]);
-        s1 += __shfl_xor(s1, 16);
-        s1 += __shfl_xor(s1, 32);
-        s2 += __shfl_xor(s2, 16);
-        s2 += __shfl_xor(s2, 32);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mx = fmaxf((float)mx2[0], (float)mx2[1]);
+        s1 = add_rows(s1);
+        s2 = add_rows(s2);
         const float mean = s1 * (1.0f / D);
         const float ex2 = s2 * (1.0f / D);
         const float var1 = ex2 - mean * mean;
-        const float th1 = fminf(fmaxf(1e-6f, p.alpha * sqrtf(fmaxf(var1, 0.f))), p.input_clip);
-        // a margin of 2^-10 covers the one-pass variance error; ill-conditioned rows
-        // (variance tiny against the mean square) always take the exact path
-        const bool flag = (n < nvalid) && (mx > th1 * (1.0f - 0.0009765625f) || var1 <= ex2 * 0.0009765625f);
+        const float th1 = fminf(fmaxf(1e-6f, p.alpha * __builtin_amdgcn_sqrtf(fmaxf(var1, 0.f))), p.input_clip);
+        // a margin of 2^-10 covers the one-pass variance error and the 1-ulp square root;
+        // ill-conditioned rows (variance tiny against the mean square) always take the
+        // exact path
+        return {mean, (n < nvalid) && (mx > th1 * (1.0f - 0.0009765625f) || var1 <= ex2 * 0.0009765625f)};
+    };
+    auto tokens = [](uint64_t m) -> uint32_t { return (uint32_t)((m | (m >> 16) | (m >> 32) | (m >> 48)) & 0xffffu); };
 
-        // ---- scores: S^T = K Q'^T (hi and lo accumulate into one column) ----
-        f4_t sc = {0.f, 0.f, 0.f, 0.f};
+    // scores S^T = K Q'^T of a tile: lane (g, n) gets tokens 4g..4g+3 of head n
+    auto qk = [&](const Frags<D>& f) -> f4_t {
+        f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < NQK; ++i) {
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[i][0][lane]), sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[i][1][lane]), sc, 0, 0, 0);
+            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[i][0][lane]), sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[i][1][lane]), sl, 0, 0, 0);
         }
+        return sh + sl;
+    };
 
-        // ---- exact scores for keys the clamp may change ----
-        if (__builtin_amdgcn_ballot_w64(flag) != 0) {
-            float part[GW];
-            float v2 = 0.f;
+    // exact fp32 scores for the flagged keys of a tile (reference clamp, two-pass variance)
+    auto exact = [&](const Frags<D>& f, const Screen& sn, const uint32_t flagged, f4_t& sc) {
+        float v2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < NQK; ++i) {
+            const uint32_t w4[4] = {f.k[i].x, f.k[i].y, f.k[i].z, f.k[i].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = half_bits_to_float((w4[e / 2] >> (16 * (e % 2))) & 0xffffu);
+                v2 = fmaf(x - sn.mean, x - sn.mean, v2);
+            }
+        }
+        v2 = add_rows(v2);
+        const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v2 * (1.0f / D))), p.input_clip);
+        float part[GW];
+#pragma unroll
+        for (int h = 0; h < GW; ++h) {
+            float a = 0.f;
 #pragma unroll
             for (int i = 0; i < NQK; ++i) {
                 const uint32_t w4[4] = {f.k[i].x, f.k[i].y, f.k[i].z, f.k[i].w};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float x = half_bits_to_float((w4[e / 2] >> (16 * (e % 2))) & 0xffffu);
-                    v2 = fmaf(x - mean, x - mean, v2);
+                    a = fmaf(qs[h][32 * i + 8 * g + e], fminf(fmaxf(x, -th), th), a);
                 }
             }
-            v2 += __shfl_xor(v2, 16);
-            v2 += __shfl_xor(v2, 32);
-            const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v2 * (1.0f / D))), p.input_clip);
-#pragma unroll
-            for (int h = 0; h < GW; ++h) {
-                float a = 0.f;
-#pragma unroll
-                for (int i = 0; i < NQK; ++i) {
-                    const uint32_t w4[4] = {f.k[i].x, f.k[i].y, f.k[i].z, f.k[i].w};
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float x = half_bits_to_float((w4[e / 2] >> (16 * (e % 2))) & 0xffffu);
-                        a = fmaf(qs[h][32 * i + 8 * g + e], fminf(fmaxf(x, -th), th), a);
-                    }
-                }
-                a += __shfl_xor(a, 16);
-                a += __shfl_xor(a, 32);
-                part[h] = a;
-            }
-            if (g == 0) {
-                patch_flag[wave][n] = flag ? 1 : 0;
-#pragma unroll
-                for (int h = 0; h < GW; ++h) patch_val[wave][n][h] = part[h];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (n < GW) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int t = 4 * g + r;
-                    if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n];
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
+            part[h] = add_rows(a);
         }
+        // Exchange through this wave's LDS slots: a wave's LDS accesses complete in
+        // program order and the compiler keeps these possibly-aliasing accesses in
+        // order, so no fence is needed.  (A fence or wave barrier here would count as
+        // a memory clobber and push the block-table reads off the scalar unit.)
+        if (g == 0) {
+            patch_flag[wave][n] = (int)((flagged >> n) & 1u);
+#pragma unroll
+            for (int h = 0; h < GW; ++h) patch_val[wave][n][h] = part[h];
+        }
+        if (n < GW) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 4 * g + r;
+                if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n];
+            }
+        }
+    };
 
-        // ---- online softmax for head n over tokens 4g..4g+3 ----
-        float s[4];
-        float mt = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float v = fminf(fmaxf(sc[r], -p.logit_clip), p.logit_clip);
-            s[r] = (n < GW && 4 * g + r < nvalid) ? v : -INFINITY;
-            mt = fmaxf(mt, s[r]);
-        }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const bool need = mt > m_run + 8.0f;
-        if (__builtin_amdgcn_ballot_w64(need) != 0) {
-            const float f = need ? exp2f(m_run - mt) : 1.0f;
-            m_run = need ? mt : m_run;
-            l_run *= f;
-#pragma unroll
-            for (int j = 0; j < NDT; ++j) acc[j] *= f;
-        }
-        float pr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            pr[r] = s[r] == -INFINITY ? 0.f : exp2f(s[r] - m_run);  // masked / unused -> 0
-            l_run += pr[r];
-        }
-        h4_t phi, plo;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const _Float16 hi = (_Float16)pr[r];
-            phi[r] = hi;
-            plo[r] = (_Float16)(pr[r] - (float)hi);
-        }
-
-        // ---- O^T += V^T P^T ----
+    // slots past the context (or a whole missing tile) may hold any bits (NaN): zero them
+    auto clear_masked_v = [&](Frags<D>& f, const int nvalid) {
         if (nvalid < kTile) {
-            // slots past the context may hold any bits (NaN): zero them
 #pragma unroll
             for (int j = 0; j < NDT; ++j) {
-                h4_t vv = as_h4(f.v[j]);
+                h4_t vv = __builtin_bit_cast(h4_t, f.v[j]);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if (4 * g + r >= nvalid) vv[r] = (_Float16)0.f;
@@ -274,30 +252,80 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
                 f.v[j] = __builtin_bit_cast(uint2, vv);
             }
         }
+    };
+
+    // one tile; a tile that is out of range or behind an invalid table entry has no
+    // valid keys and contributes nothing
+    auto process = [&](Frags<D>& f, const bool ok, const int tile) {
+        const int nvalid = ok ? min(kTile, ctx - tile * kTile) : 0;
+        const Screen sn = screen(f, nvalid);
+        f4_t sc = qk(f);
+        const uint32_t flagged = tokens(__builtin_amdgcn_ballot_w64(sn.flag));
+        if (flagged != 0u) exact(f, sn, flagged, sc);
+
+        // ---- online softmax for head n over tokens 4g..4g+3.  The running max moves
+        // only when a score exceeds it by more than 8 (p stays <= 2^8), so the
+        // cross-lane max is taken only then. ----
+        float s[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] = __builtin_amdgcn_fmed3f(sc[r], clip_lo, clip_hi);
+        if (nvalid < kTile) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] = 4 * g + r < nvalid ? s[r] : -INFINITY;
+            clear_masked_v(f, nvalid);
+        }
+        const float smax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        if (__builtin_amdgcn_ballot_w64(smax > m_run + 8.0f) != 0) {
+            const float mt = max_rows(smax);
+            const bool need = mt > m_run + 8.0f;
+            const float fct = need ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
+            m_run = need ? mt : m_run;
+            l_run *= fct;
+#pragma unroll
+            for (int j = 0; j < NDT; ++j) acc[j] *= fct;
+        }
+        // v_exp_f32 of -inf is +0: masked tokens and unused columns drop out
+        h4_t phi, plo;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float pv = __builtin_amdgcn_exp2f(s[r] - m_run);
+            l_run += pv;
+            const _Float16 hi = (_Float16)pv;
+            phi[r] = hi;
+            plo[r] = (_Float16)(pv - (float)hi);
+        }
+
+        // ---- O^T += V^T P^T ----
 #pragma unroll
         for (int j = 0; j < NDT; ++j) {
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(f.v[j]), phi, acc[j], 0, 0, 0);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(f.v[j]), plo, acc[j], 0, 0, 0);
+            const h4_t a = __builtin_bit_cast(h4_t, f.v[j]);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, phi, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, plo, acc[j], 0, 0, 0);
         }
     };
 
-    // two tiles in flight per wave: buffers A and B alternate, so a tile's loads are
-    // issued two tiles before it is processed and no registers are copied
-    Frags<D> fa, fb;
-    int tile = tile_begin + wave;
-    bool oka = tile < tile_end ? load(tile, fa) : false;
-    bool okb = tile + kWaves < tile_end ? load(tile + kWaves, fb) : false;
-    for (; tile < tile_end; tile += 2 * kWaves) {
-        if (oka) process(fa, tile);
-        oka = tile + 2 * kWaves < tile_end ? load(tile + 2 * kWaves, fa) : false;
-        if (tile + kWaves >= tile_end) break;
-        if (okb) process(fb, tile + kWaves);
-        okb = tile + 3 * kWaves < tile_end ? load(tile + 3 * kWaves, fb) : false;
+    // NB tiles in flight per wave: buffer u holds tile t0 + (k + u) * kWaves and is
+    // reloaded with the tile NB steps ahead right after it is processed.  The trip
+    // count is uniform (rounded up to NB; the extra tiles are out of range and fully
+    // masked) and every step loads and processes unconditionally, so the compiler's
+    // wait counts stay exact.
+    const int t0 = tile_begin + wave;
+    const int nt = t0 < tile_end ? (tile_end - t0 + kWaves - 1) / kWaves : 0;
+    Frags<D> f[NB];
+    bool ok[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * kWaves, f[u]);
+    for (int k = 0; k < nt; k += NB) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int t = t0 + (k + u) * kWaves;
+            process(f[u], ok[u], t);
+            ok[u] = load(t + NB * kWaves, f[u]);
+        }
     }
 
     // ---- wave result: column n < GW holds head n; lane (g, n) has d = 16j + 4g + r ----
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = add_rows(l_run);
     if (n < GW) {
 #pragma unroll
         for (int j = 0; j < NDT; ++j) {
@@ -310,44 +338,20 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         }
     }
     __syncthreads();
-
-    // ---- merge the waves of this workgroup ----
-    for (int idx = threadIdx.x; idx < GW * D; idx += 256) {
-        const int h = idx / D;
-        const int d = idx % D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[w][h][0]);
-        float a = 0.f, l = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = comb[w][h][0];
-            if (mw != -INFINITY) {
-                const float f = exp2f(mw - M);
-                a = fmaf(comb[w][h][2 + d], f, a);
-                l = fmaf(comb[w][h][1], f, l);
-            }
-        }
-        const size_t hq = (size_t)b * p.hq + hq0 + h;
-        if (nparts == 1) {
-            p.out[hq * D + d] = l > 0.f ? a / l : 0.f;
-        } else {
-            const size_t slot = hq * p.max_parts + part;
-            p.part_acc[slot * D + d] = a;
-            if (d == 0) {
-                p.part_ml[2 * slot] = M;
-                p.part_ml[2 * slot + 1] = l;
-            }
-        }
-    }
+    merge_waves<D, GW>(p, comb, b, hq0, part, nparts);
 }
+
+#ifndef VSPEC_F16_TILES_IN_FLIGHT
+#define VSPEC_F16_TILES_IN_FLIGHT 2
+#endif
 
 template <int D, int GW>
 void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
+    constexpr int NB = VSPEC_F16_TILES_IN_FLIGHT;
     if (p.block_tokens == 16) {
-        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 16>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 16, NB>), grid, dim3(256), 0, s, p);
     } else {
-        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0, NB>), grid, dim3(256), 0, s, p);
     }
 }
 

@@ -273,14 +273,15 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             for (int i = 0; i < 8 * NQ; ++i) a = fmaf(qs[h][8 * g * NQ + i], fminf(fmaxf(x[i], -th), th), a);
             part[h] = add_rows(a);
         }
+        // Exchange through this wave's LDS slots: a wave's LDS accesses complete in
+        // program order and the compiler keeps these possibly-aliasing accesses in
+        // order, so no fence is needed.  (A fence or wave barrier here would count as
+        // a memory clobber and push the block-table reads off the scalar unit.)
         if (g == 0) {
             patch_flag[wave][n] = (int)((flagged >> n) & 1u);
 #pragma unroll
             for (int h = 0; h < GW; ++h) patch_val[wave][n][h] = part[h];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (n < GW) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -288,8 +289,6 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n];
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
     };
 
     // Slots past the context (or a whole missing tile) may hold any scale bits (NaN):
