@@ -72,6 +72,39 @@ int vspec_rocm_paged_page_info(const VspecRocmPagedMeta* m, size_t page, uint32_
 int vspec_rocm_paged_block_table(const VspecRocmPagedMeta* m, uint64_t session_id, int32_t* out,
                                  size_t cap, uint32_t* ctx_len);
 
+/* A continuous-batching work item: same fields and layout as VspecContinuousBatchItem
+ * (continuous_batch.h:15-20).  request_id doubles as the paged-cache session id;
+ * phase is 1 (prefill) or 2 (decode); token_quota new tokens enter the cache. */
+typedef struct VspecRocmStepItem {
+    uint64_t request_id;
+    uint32_t phase;
+    size_t token_quota;
+    size_t prompt_cursor;
+} VspecRocmStepItem;
+
+/* Plan one step of continuous batching: reserve each item's token_quota tokens and
+ * emit, per item i, its block table row (block_tables[i*max_blocks ..], -1 padded), its
+ * context after the step (ctx_lens[i]) and the position of its first new token
+ * (start_pos[i]); and, per packed new token t (items in order, quota tokens each), its
+ * item (token_item[t]) and position (token_pos[t]) -- the inputs of
+ * vspec_rocm_kv_append_tokens and of the decode descriptor.  Returns 0 on a repeated
+ * request, a failed reservation, an eviction of an earlier item's session by a later
+ * one, a session that is not a block table (shared partly filled middle page), or
+ * outputs that are too small; reservations made before the failure stay made. */
+int vspec_rocm_paged_plan_step(VspecRocmPagedMeta* m, const VspecRocmStepItem* items,
+                               size_t n_items, int32_t* block_tables, size_t max_blocks,
+                               int32_t* ctx_lens, int32_t* start_pos, int32_t* token_item,
+                               int32_t* token_pos, size_t max_tokens, size_t* n_tokens);
+
+/* Append packed new tokens (device pointers): token t of k_new/v_new ([n][H][D] in
+ * src_dtype) goes to position token_pos[t] of the sequence whose block table is row
+ * token_item[t] of block_tables.  Mixed chunked-prefill and decode steps append in
+ * one launch; quantises on write for int4 pools. */
+int vspec_rocm_kv_append_tokens(const VspecPagedKV* kv, uint32_t n_tokens, const int32_t* token_item,
+                                const int32_t* token_pos, const int32_t* block_tables,
+                                uint32_t max_blocks_per_seq, const void* k_new, const void* v_new,
+                                int32_t src_dtype, void* stream);
+
 /* ---- GPU-resident handles with the reference Python C-API signatures ---- */
 int vspec_py_kv_cache_create(size_t page_tokens, size_t max_pages, size_t num_heads, size_t head_dim);
 void vspec_py_kv_cache_destroy(int handle_id);

@@ -270,6 +270,13 @@ class Reference:
             "vr_int3_append_and_dump": (C.c_int, [_f32p, _f32p, _sz, _sz, _sz, _sz, _u8p, _f32p, _f32p]),
             "vr_now": (C.c_double, []),
             "vr_baseline_decode": (C.c_double, [C.c_int, _sz, _sz, _sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p]),
+            "vr_batcher_new": (_vp, [_sz, _sz, _sz, _sz, _sz, _sz]),
+            "vr_batcher_free": (None, [_vp]),
+            "vr_batch_item_size": (_sz, []),
+            "vspec_continuous_batch_submit": (C.c_int, [_vp, _sz, _sz, _sz, C.c_uint16, C.POINTER(C.c_uint64)]),
+            "vspec_continuous_batch_next_batch": (_sz, [_vp, _vp, _sz]),
+            "vspec_continuous_batch_commit_prefill": (C.c_int, [_vp, C.c_uint64, _sz]),
+            "vspec_continuous_batch_commit_decode": (C.c_int, [_vp, C.c_uint64, _sz, C.c_int]),
             "vspec_kv_paged_open_session": (C.c_int, [_vp, C.c_uint64]),
             "vspec_kv_paged_close_session": (C.c_int, [_vp, C.c_uint64]),
             "vspec_kv_paged_reuse_prefix": (C.c_int, [_vp, C.c_uint64, C.c_uint64, _sz]),

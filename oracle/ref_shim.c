@@ -265,3 +265,20 @@ double vr_baseline_decode(int nthreads, size_t nseq, size_t T, size_t hq, size_t
     free(th);
     return elapsed;
 }
+
+/* ---- continuous-batching scheduler (continuous_batch.c) behind an opaque pointer ---- */
+#include "vspec/runtime/continuous_batch.h"
+
+VspecContinuousBatcher* vr_batcher_new(size_t total_vram_bytes, size_t max_active, size_t max_batch_items,
+                                       size_t max_batch_tokens, size_t prefill_quantum, size_t decode_quantum) {
+    VspecContinuousBatcher* b = (VspecContinuousBatcher*)calloc(1, sizeof(VspecContinuousBatcher));
+    if (b) {
+        vspec_continuous_batch_init(b, total_vram_bytes, max_active, max_batch_items, max_batch_tokens,
+                                    prefill_quantum, decode_quantum);
+    }
+    return b;
+}
+
+void vr_batcher_free(VspecContinuousBatcher* b) { free(b); }
+
+size_t vr_batch_item_size(void) { return sizeof(VspecContinuousBatchItem); }

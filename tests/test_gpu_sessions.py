@@ -166,3 +166,54 @@ def test_decode_over_handle_pool(ref, gpu, mode):
             assert err <= 1e-4, (s, err)
     finally:
         cache.close()
+
+
+@pytest.mark.parametrize("dtype", [1, 2])  # f16, int4 pools
+def test_continuous_batching_steps(oracle, ref, gpu, dtype):
+    """Steps of the reference scheduler (continuous_batch.c) run end to end: the host
+    allocator plans each step, one packed append writes the mixed chunked-prefill and
+    decode tokens (quantised on write for int4), and the decode-phase items attend over
+    their caches.  The pool matches the oracle's bit for bit after every step and the
+    outputs match the oracle's attention (4e-3)."""
+    import torch
+    import vspec_rocm as vr
+    from oracle.oracle import HostPool
+    from test_paged_meta_cpu import _ref_batcher_steps
+    from vspec_rocm.sessions import plan_step
+
+    P, MAXP, Hkv, Hq, D = 16, 96, 2, 8, 128
+    m = vr.lib().vspec_rocm_paged_meta_create(P, MAXP, 0, 0)
+    pool = vr.PagedPool(dtype, MAXP, P, Hkv, D, device=gpu)
+    host = HostPool(dtype, MAXP, P, Hkv, D)
+    rng = np.random.default_rng(10 + dtype)
+    try:
+        for si, step in enumerate(_ref_batcher_steps(ref, 20 + dtype, n_req=5, max_items=6, max_tokens=48,
+                                                     prefill_q=24)):
+            plan = plan_step(m, step, max_blocks=16)
+            n = plan["token_item"].size
+            k16 = oracle.f32_to_f16(rng.standard_normal((n, Hkv, D)).astype(np.float32))
+            v16 = oracle.f32_to_f16(rng.standard_normal((n, Hkv, D)).astype(np.float32))
+            tabs = plan["block_tables"]
+            for i, it in enumerate(step):  # oracle: per item, its tokens in order
+                sel = np.flatnonzero(plan["token_item"] == i)
+                assert oracle.paged_append(host, np.ascontiguousarray(tabs[i:i + 1]), plan["start_pos"][i:i + 1],
+                                           np.ascontiguousarray(k16[sel][None]), np.ascontiguousarray(v16[sel][None]))
+            dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+            kd = torch.from_numpy(k16.view(np.int16)).to(gpu).view(torch.float16)
+            vd = torch.from_numpy(v16.view(np.int16)).to(gpu).view(torch.float16)
+            vr.kv_append_tokens(pool, dev(plan["token_item"]), dev(plan["token_pos"]), dev(tabs), kd, vd)
+            torch.cuda.synchronize()
+            from test_gpu_parity import assert_pools_equal
+            assert_pools_equal(host, pool)
+            dec = [i for i, it in enumerate(step) if it.phase == 2]
+            if dec:
+                q = rng.standard_normal((len(dec), Hq, D)).astype(np.float32)
+                t_sub = np.ascontiguousarray(tabs[dec])
+                c_sub = np.ascontiguousarray(plan["ctx_lens"][dec])
+                got = vr.paged_decode(pool, dev(t_sub), dev(c_sub), dev(q), numerics=si % 2).cpu().numpy()
+                want = oracle.paged_decode(si % 2, host, t_sub, c_sub, q)
+                err = float(np.abs(got - want).max())
+                assert err <= 4e-3, (si, err)
+        say(f"[cb] dtype={dtype} steps={si + 1}")
+    finally:
+        vr.lib().vspec_rocm_paged_meta_destroy(m)

@@ -157,3 +157,95 @@ def test_block_table_refuses_partial_middle_pages(lib):
     assert not lib.vspec_rocm_paged_block_table(m, 2, tab, 8, None)
     assert lib.vspec_rocm_paged_block_table(m, 1, tab, 8, None)
     lib.vspec_rocm_paged_meta_destroy(m)
+
+
+def _ref_batcher_steps(ref, seed, n_req=6, max_items=8, max_tokens=64, prefill_q=32):
+    """Drive the reference continuous batcher (continuous_batch.c) to completion,
+    yielding each step's items and committing them afterwards."""
+    import vspec_rocm
+
+    assert ref.lib.vr_batch_item_size() == C.sizeof(vspec_rocm.VspecRocmStepItem)
+    rng = np.random.default_rng(seed)
+    bt = ref.lib.vr_batcher_new(1 << 40, 16, max_items, max_tokens, prefill_q, 1)
+    try:
+        rid = C.c_uint64()
+        for _ in range(n_req):
+            assert ref.lib.vspec_continuous_batch_submit(bt, 1 << 20, int(rng.integers(1, 150)),
+                                                         int(rng.integers(1, 12)), 0, C.byref(rid))
+        items = (vspec_rocm.VspecRocmStepItem * max_items)()
+        for _ in range(400):
+            k = ref.lib.vspec_continuous_batch_next_batch(bt, items, max_items)
+            if k == 0:
+                return
+            step = [vspec_rocm.VspecRocmStepItem(items[i].request_id, items[i].phase, items[i].token_quota,
+                                                 items[i].prompt_cursor) for i in range(k)]
+            yield step
+            for it in step:
+                if it.phase == 1:
+                    assert ref.lib.vspec_continuous_batch_commit_prefill(bt, it.request_id, it.token_quota)
+                else:
+                    assert ref.lib.vspec_continuous_batch_commit_decode(bt, it.request_id, it.token_quota, 0)
+        raise AssertionError("batcher did not drain")
+    finally:
+        ref.lib.vr_batcher_free(bt)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_plan_step_follows_reference_scheduler(lib, ref, seed):
+    """Steps of the reference scheduler planned on the host allocator: the packed token
+    map, start positions and context lengths are consistent, and every position of every
+    item maps through its block table to the page and slot the reference paged cache
+    (appending the same tokens) holds it in."""
+    from vspec_rocm.sessions import plan_step
+
+    P, MAXP, H, D = 16, 512, 1, 8
+    m = lib.vspec_rocm_paged_meta_create(P, MAXP, 0, 0)
+    c = ref.lib.vr_paged_new(P, MAXP, H, D)
+    tok = np.zeros(H * D, np.float32)
+    nsteps = 0
+    try:
+        for step in _ref_batcher_steps(ref, seed):
+            nsteps += 1
+            plan = plan_step(m, step, max_blocks=64)
+            off = 0
+            for i, it in enumerate(step):
+                q = int(it.token_quota)
+                assert (plan["token_item"][off:off + q] == i).all()
+                assert (plan["token_pos"][off:off + q] == plan["start_pos"][i] + np.arange(q)).all()
+                assert plan["ctx_lens"][i] == plan["start_pos"][i] + q
+                off += q
+                for _ in range(q):
+                    assert ref.lib.vspec_kv_paged_append(c, it.request_id, tok.ctypes.data_as(_f32p),
+                                                         tok.ctypes.data_as(_f32p))
+            assert off == plan["token_item"].size
+            for i, it in enumerate(step):
+                n = int(plan["ctx_lens"][i])
+                assert n == ref.lib.vspec_kv_paged_session_tokens(c, it.request_id)
+                for t in range(n):
+                    want = _ref_locate(ref, c, P, H, D, it.request_id, t)
+                    assert want == (int(plan["block_tables"][i, t // P]), t % P), (i, t)
+        assert nsteps > 5
+    finally:
+        lib.vspec_rocm_paged_meta_destroy(m)
+        ref.lib.vr_paged_free(c)
+
+
+def test_plan_step_rejects_bad_steps(lib):
+    from vspec_rocm import VspecRocmError
+    from vspec_rocm.sessions import plan_step
+
+    m = lib.vspec_rocm_paged_meta_create(4, 3, 0, 0)
+    try:
+        with pytest.raises(VspecRocmError):
+            plan_step(m, [(7, 2, 1, 0), (7, 2, 1, 0)], max_blocks=4)  # repeated request
+        with pytest.raises(VspecRocmError):
+            plan_step(m, [(8, 1, 9, 0)], max_blocks=2)  # 9 tokens need 3 pages > 2 columns
+        # pool of 3 pages: the second item's pages evict the first item's session
+        m2 = lib.vspec_rocm_paged_meta_create(4, 3, 0, 0)
+        try:
+            with pytest.raises(VspecRocmError):
+                plan_step(m2, [(1, 1, 8, 0), (2, 1, 8, 0)], max_blocks=4)
+        finally:
+            lib.vspec_rocm_paged_meta_destroy(m2)
+    finally:
+        lib.vspec_rocm_paged_meta_destroy(m)

@@ -359,6 +359,10 @@ struct AppendParams {
     uint16_t* vs;
     const int32_t* block_tables;
     const int32_t* start_pos;
+    // packed-token mode (token_item != null): source token b (n_new == 1) goes to
+    // position token_pos[b] of block-table row token_item[b]
+    const int32_t* token_item;
+    const int32_t* token_pos;
     const uint8_t* k_new;
     const uint8_t* v_new;
     uint32_t batch;
@@ -388,12 +392,13 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
         const uint32_t i = (uint32_t)(r % p.n_new);
         const uint32_t b = (uint32_t)(r / p.n_new);
 
-        const int32_t sp = p.start_pos[b];
-        if (sp < 0) continue;
+        const uint32_t seq = p.token_item ? (uint32_t)p.token_item[b] : b;
+        const int32_t sp = p.token_item ? p.token_pos[b] : p.start_pos[b];
+        if (sp < 0 || (p.token_item && p.token_item[b] < 0)) continue;
         const uint32_t pos = (uint32_t)sp + i;
         const uint32_t lb = pos / p.block_tokens;
         if (lb >= p.max_blocks) continue;
-        const int32_t phys = p.block_tables[(size_t)b * p.max_blocks + lb];
+        const int32_t phys = p.block_tables[(size_t)seq * p.max_blocks + lb];
         if (phys < 0 || (uint32_t)phys >= p.num_blocks) continue;
         const uint32_t slot = pos % p.block_tokens;
         const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + slot;
@@ -949,37 +954,18 @@ void vspec_rocm_kv_pool_destroy(VspecPagedKV* kv) {
     memset(kv, 0, sizeof(*kv));
 }
 
-int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
-                         uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
-                         const void* k_new, const void* v_new, int32_t src_dtype, void* stream) {
-    if (!check_kv(kv, "kv_append")) return 0;
-    if (src_dtype != VSPEC_KV_F32 && src_dtype != VSPEC_KV_F16) {
-        set_err("kv_append: src_dtype must be f32 or f16");
-        return 0;
-    }
-    if (batch == 0 || n_new == 0) return 1;
-    if (!block_tables || !start_pos || !k_new || !v_new || max_blocks_per_seq == 0) {
-        set_err("kv_append: null argument");
-        return 0;
-    }
-    AppendParams p;
+static int append_launch(const char* who, const VspecPagedKV* kv, AppendParams& p, int32_t src_dtype,
+                         void* stream) {
     p.k = (uint8_t*)kv->k_data;
     p.v = (uint8_t*)kv->v_data;
     p.ks = kv->k_scales;
     p.vs = kv->v_scales;
-    p.block_tables = block_tables;
-    p.start_pos = start_pos;
-    p.k_new = (const uint8_t*)k_new;
-    p.v_new = (const uint8_t*)v_new;
-    p.batch = batch;
-    p.n_new = n_new;
     p.hkv = kv->num_kv_heads;
     p.head_dim = kv->head_dim;
     p.block_tokens = kv->block_tokens;
-    p.max_blocks = max_blocks_per_seq;
     p.num_blocks = kv->num_blocks;
     const uint32_t ept = kv->dtype == VSPEC_KV_INT4 ? 32 : 8;
-    const uint64_t items = (uint64_t)batch * n_new * kv->num_kv_heads * (kv->head_dim / ept) * 2;
+    const uint64_t items = (uint64_t)p.batch * p.n_new * kv->num_kv_heads * (kv->head_dim / ept) * 2;
     uint64_t blocks = (items + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     const dim3 grid((unsigned)blocks);
@@ -995,8 +981,58 @@ int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* 
         else VSPEC_APPEND(VSPEC_KV_INT4, VSPEC_KV_F16);
     }
 #undef VSPEC_APPEND
-    HIP_CHECK(hipGetLastError(), "kv_append launch");
+    HIP_CHECK(hipGetLastError(), who);
     return 1;
+}
+
+int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                         uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                         const void* k_new, const void* v_new, int32_t src_dtype, void* stream) {
+    if (!check_kv(kv, "kv_append")) return 0;
+    if (src_dtype != VSPEC_KV_F32 && src_dtype != VSPEC_KV_F16) {
+        set_err("kv_append: src_dtype must be f32 or f16");
+        return 0;
+    }
+    if (batch == 0 || n_new == 0) return 1;
+    if (!block_tables || !start_pos || !k_new || !v_new || max_blocks_per_seq == 0) {
+        set_err("kv_append: null argument");
+        return 0;
+    }
+    AppendParams p = {};
+    p.block_tables = block_tables;
+    p.start_pos = start_pos;
+    p.k_new = (const uint8_t*)k_new;
+    p.v_new = (const uint8_t*)v_new;
+    p.batch = batch;
+    p.n_new = n_new;
+    p.max_blocks = max_blocks_per_seq;
+    return append_launch("kv_append launch", kv, p, src_dtype, stream);
+}
+
+int vspec_rocm_kv_append_tokens(const VspecPagedKV* kv, uint32_t n_tokens, const int32_t* token_item,
+                                const int32_t* token_pos, const int32_t* block_tables,
+                                uint32_t max_blocks_per_seq, const void* k_new, const void* v_new,
+                                int32_t src_dtype, void* stream) {
+    if (!check_kv(kv, "kv_append_tokens")) return 0;
+    if (src_dtype != VSPEC_KV_F32 && src_dtype != VSPEC_KV_F16) {
+        set_err("kv_append_tokens: src_dtype must be f32 or f16");
+        return 0;
+    }
+    if (n_tokens == 0) return 1;
+    if (!token_item || !token_pos || !block_tables || !k_new || !v_new || max_blocks_per_seq == 0) {
+        set_err("kv_append_tokens: null argument");
+        return 0;
+    }
+    AppendParams p = {};
+    p.block_tables = block_tables;
+    p.token_item = token_item;
+    p.token_pos = token_pos;
+    p.k_new = (const uint8_t*)k_new;
+    p.v_new = (const uint8_t*)v_new;
+    p.batch = n_tokens;
+    p.n_new = 1;
+    p.max_blocks = max_blocks_per_seq;
+    return append_launch("kv_append_tokens launch", kv, p, src_dtype, stream);
 }
 
 int vspec_rocm_kv_gather(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,

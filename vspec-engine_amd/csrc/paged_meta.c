@@ -321,3 +321,55 @@ int vspec_rocm_paged_block_table(const VspecRocmPagedMeta* m, uint64_t id, int32
     if (ctx_len) *ctx_len = (uint32_t)s->total_tokens;
     return 1;
 }
+
+/* One continuous-batching step (the items of vspec_continuous_batch_next_batch,
+ * continuous_batch.c:155-270): reserve every item's token_quota new tokens, then emit
+ * the kernels' inputs.  Items are processed in order; item i's new tokens are packed
+ * at [sum of earlier quotas, + quota).  Fails when an item repeats a request, a
+ * reservation fails, a later reservation evicted an earlier item's session, a session
+ * cannot be expressed as a block table (a shared, partly filled page in the middle),
+ * or an output is too small.  Reservations made before a failure stay made, as with a
+ * sequence of reference appends that stops at its first failure. */
+int vspec_rocm_paged_plan_step(VspecRocmPagedMeta* m, const VspecRocmStepItem* items,
+                               size_t n_items, int32_t* block_tables, size_t max_blocks,
+                               int32_t* ctx_lens, int32_t* start_pos, int32_t* token_item,
+                               int32_t* token_pos, size_t max_tokens, size_t* n_tokens) {
+    if (!m || (n_items && (!items || !block_tables || !ctx_lens || !start_pos)) || max_blocks == 0) {
+        return 0;
+    }
+    size_t total = 0;
+    for (size_t i = 0; i < n_items; ++i) {
+        for (size_t j = 0; j < i; ++j) {
+            if (items[j].request_id == items[i].request_id) return 0;
+        }
+        if (items[i].token_quota > (size_t)INT32_MAX || total + items[i].token_quota > max_tokens) return 0;
+        total += items[i].token_quota;
+    }
+    if (total && (!token_item || !token_pos)) return 0;
+    size_t off = 0;
+    for (size_t i = 0; i < n_items; ++i) {
+        const uint64_t id = items[i].request_id;
+        if (!vspec_rocm_paged_open_session(m, id)) return 0;
+        const size_t before = vspec_rocm_paged_session_tokens(m, id);
+        if (before + items[i].token_quota > (size_t)INT32_MAX) return 0;
+        start_pos[i] = (int32_t)before;
+        for (size_t t = 0; t < items[i].token_quota; ++t) {
+            if (!vspec_rocm_paged_reserve(m, id, NULL, NULL)) return 0;
+            token_item[off + t] = (int32_t)i;
+            token_pos[off + t] = (int32_t)(before + t);
+        }
+        off += items[i].token_quota;
+    }
+    for (size_t i = 0; i < n_items; ++i) {
+        const uint64_t id = items[i].request_id;
+        /* an eviction triggered by a later item restarts this session's count */
+        if (vspec_rocm_paged_session_tokens(m, id) != (size_t)start_pos[i] + items[i].token_quota) return 0;
+        int32_t* row = block_tables + i * max_blocks;
+        for (size_t k = 0; k < max_blocks; ++k) row[k] = -1;
+        uint32_t ctx = 0;
+        if (!vspec_rocm_paged_block_table(m, id, row, max_blocks, &ctx)) return 0;
+        ctx_lens[i] = (int32_t)ctx;
+    }
+    if (n_tokens) *n_tokens = total;
+    return 1;
+}

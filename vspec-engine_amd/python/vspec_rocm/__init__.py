@@ -126,6 +126,17 @@ class VspecRocmPagedStats(C.Structure):
     ]
 
 
+class VspecRocmStepItem(C.Structure):
+    """Same layout as the reference's VspecContinuousBatchItem (continuous_batch.h:15-20)."""
+
+    _fields_ = [
+        ("request_id", C.c_uint64),
+        ("phase", C.c_uint32),
+        ("token_quota", C.c_size_t),
+        ("prompt_cursor", C.c_size_t),
+    ]
+
+
 _u32p = C.POINTER(C.c_uint32)
 _i32p_ = C.POINTER(C.c_int32)
 _f32p = C.POINTER(C.c_float)
@@ -168,6 +179,10 @@ SIGNATURES = {
     "vspec_py_kv_cache_meta": (_vp, [C.c_int]),
     "vspec_py_kv_cache_pool": (C.POINTER(VspecPagedKV), [C.c_int]),
     "vspec_rocm_kv_gather_rows": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, _vp, _vp]),
+    "vspec_rocm_paged_plan_step": (C.c_int, [_vp, C.POINTER(VspecRocmStepItem), C.c_size_t, _i32p_, C.c_size_t, _i32p_,
+                                             _i32p_, _i32p_, _i32p_, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "vspec_rocm_kv_append_tokens": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, C.c_uint32, _vp, _vp,
+                                              C.c_int32, _vp]),
 }
 
 _LIB = None
@@ -262,6 +277,24 @@ def kv_append(pool: PagedPool, block_tables, start_pos, k_new, v_new, stream=Non
     d = pool.desc()
     _check(lib().vspec_rocm_kv_append(C.byref(d), B, bt.data_ptr(), bt.shape[1], sp.data_ptr(), n_new,
                                       k_new.data_ptr(), v_new.data_ptr(), src, _stream(stream)), "kv_append")
+
+
+def kv_append_tokens(pool, token_item, token_pos, block_tables, k_new, v_new, stream=None):
+    """vspec_rocm_kv_append_tokens: packed new tokens k_new/v_new [n][H][D] (float32 or
+    float16, device); token t goes to position token_pos[t] of block-table row
+    token_item[t]."""
+    import torch
+
+    n = int(token_item.numel())
+    if n == 0:
+        return
+    assert k_new.is_contiguous() and v_new.is_contiguous() and k_new.shape[0] == n
+    src = KV_F16 if k_new.dtype == torch.float16 else KV_F32
+    bt = block_tables.to(torch.int32).contiguous()
+    kv = pool.desc()
+    _check(lib().vspec_rocm_kv_append_tokens(C.byref(kv), n, token_item.data_ptr(), token_pos.data_ptr(),
+                                             bt.data_ptr(), bt.shape[1], k_new.data_ptr(), v_new.data_ptr(), src,
+                                             _stream(stream)), "kv_append_tokens")
 
 
 def kv_gather(pool: PagedPool, block_tables, ctx_lens, out_mode=GATHER_RAW, max_ctx_len=None, stream=None):

@@ -17,7 +17,7 @@ import ctypes as C
 
 import numpy as np
 
-from . import VspecPagedKV, VspecRocmError, VspecRocmPagedStats, last_error, lib
+from . import VspecPagedKV, VspecRocmError, VspecRocmPagedStats, VspecRocmStepItem, last_error, lib
 
 _f32p = C.POINTER(C.c_float)
 
@@ -134,3 +134,36 @@ class CorePagedKVCache:
             self.close()
         except Exception:
             pass
+
+
+def plan_step(meta, items, max_blocks: int, max_tokens: int | None = None):
+    """vspec_rocm_paged_plan_step over a VspecRocmPagedMeta* (e.g. CorePagedKVCache._meta()).
+
+    items: sequence of (request_id, phase, token_quota, prompt_cursor) or VspecRocmStepItem.
+    Returns dict(block_tables [n][max_blocks], ctx_lens [n], start_pos [n], token_item [t],
+    token_pos [t]) as int32 numpy arrays; raises VspecRocmError when the step cannot be
+    planned."""
+    n = len(items)
+    arr = (VspecRocmStepItem * max(n, 1))()
+    for i, it in enumerate(items):
+        if isinstance(it, VspecRocmStepItem):
+            arr[i] = it
+        else:
+            arr[i] = VspecRocmStepItem(*[int(x) for x in it])
+    total = sum(int(arr[i].token_quota) for i in range(n))
+    cap = total if max_tokens is None else int(max_tokens)
+    tables = np.full((max(n, 1), max_blocks), -1, np.int32)
+    ctx = np.zeros(max(n, 1), np.int32)
+    start = np.zeros(max(n, 1), np.int32)
+    titem = np.zeros(max(cap, 1), np.int32)
+    tpos = np.zeros(max(cap, 1), np.int32)
+    got = C.c_size_t()
+    p32 = lambda a: a.ctypes.data_as(C.POINTER(C.c_int32))
+    ok = lib().vspec_rocm_paged_plan_step(meta, arr, n, p32(tables), max_blocks, p32(ctx), p32(start), p32(titem),
+                                          p32(tpos), cap, C.byref(got))
+    if not ok:
+        raise VspecRocmError("plan_step failed (pool exhausted, eviction of a batch member, repeated request, "
+                             "shared partly filled page, or outputs too small)")
+    t = int(got.value)
+    return dict(block_tables=tables[:n], ctx_lens=ctx[:n], start_pos=start[:n], token_item=titem[:t],
+                token_pos=tpos[:t])
