@@ -77,6 +77,21 @@ int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* 
                          uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
                          const void* k_new, const void* v_new, int32_t src_dtype, void* stream);
 
+/* ---- rotary embedding fused with the append: runtime_inference.py:1303-1313 (q, k
+ * rotated by the cached cos/sin of the token position, :1186-1192) then the append ----
+ * As vspec_rocm_kv_append, with K rotated before it is stored: pairs (i, i + rope_dim/2)
+ * of the first rope_dim elements become (x1*c - x2*s, x1*s + x2*c) with c, s from row
+ * `position` of the device fp32 tables rope_cos / rope_sin [max_pos][rope_dim/2]; every
+ * product and sum is rounded separately (fp32), as numpy's float32 arithmetic does.
+ * When q_in is given ([batch][n_new][num_q_heads][D] fp32, device) its rows are rotated
+ * into q_out the same way.  A token whose position has no table row is not written. */
+int vspec_rocm_kv_append_rope(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                              uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                              const void* k_new, const void* v_new, int32_t src_dtype,
+                              const float* rope_cos, const float* rope_sin, uint32_t rope_dim,
+                              uint32_t max_pos, const float* q_in, float* q_out,
+                              uint32_t num_q_heads, void* stream);
+
 /* ---- gather: vspec_py_kv_cache_read (capi.c:2263-2299) for a batch ----
  * Sequence b's tokens 0..ctx_lens[b]-1 go to output tokens out_token_offset[b]+t in
  * [T][H][D] order.  out_mode VSPEC_GATHER_RAW copies the pool format (f32, f16, or

@@ -124,6 +124,9 @@ class Oracle:
             "vo_paged_compact": (C.c_int, [C.POINTER(VoPagedKV), C.c_uint32, _i32p, _i32p]),
             "vo_paged_decode_attention": (C.c_int, [C.c_int, _sz, C.POINTER(VoPagedKV), C.c_uint32, C.c_uint32, _i32p, C.c_uint32, _i32p, _f32p, _f32p]),
             "vo_attention_textbook_f64": (None, [_f32p, _f32p, _sz, _f32p, _sz, _sz, _sz, C.POINTER(C.c_double)]),
+            "vo_rope_row": (None, [_f32p, _f32p, _sz, _sz, _f32p, _f32p]),
+            "vo_paged_append_rope": (C.c_int, [C.POINTER(VoPagedKV), C.c_uint32, _i32p, C.c_uint32, _i32p, C.c_uint32,
+                                               _vp, _vp, C.c_int, _f32p, _f32p, _sz, _sz]),
             "vo_int4_ks_index": (_sz, [C.POINTER(VoPagedKV), _sz, _sz, _sz, _sz]),
             "vo_int4_v_byte": (_sz, [C.POINTER(VoPagedKV), _sz, _sz, _sz, _sz, C.POINTER(C.c_int)]),
         }
@@ -192,6 +195,27 @@ class Oracle:
         out = np.zeros((H, D), np.float32)
         self.lib.vo_attention_ref_single_query(mode, dot_block, ptr(q, _f32p), ptr(k, _f32p), ptr(v, _f32p), T, H, D, ptr(out, _f32p))
         return out
+
+    def rope_row(self, x, rope_dim, cos_row, sin_row):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.vo_rope_row(ptr(x, _f32p), ptr(out, _f32p), x.size, rope_dim,
+                             ptr(np.ascontiguousarray(cos_row, np.float32), _f32p),
+                             ptr(np.ascontiguousarray(sin_row, np.float32), _f32p))
+        return out
+
+    def paged_append_rope(self, pool: HostPool, block_tables, start_pos, k_new, v_new, cos, sin, rope_dim):
+        """paged_append with K rotated by rows start_pos+i of cos/sin [max_pos][rope_dim/2]."""
+        B, n_new = k_new.shape[0], k_new.shape[1]
+        bt = np.ascontiguousarray(block_tables, np.int32)
+        sp = np.ascontiguousarray(start_pos, np.int32)
+        src_dtype = 0 if k_new.dtype == np.float32 else 1
+        cos = np.ascontiguousarray(cos, np.float32)
+        sin = np.ascontiguousarray(sin, np.float32)
+        d = pool.desc()
+        return bool(self.lib.vo_paged_append_rope(C.byref(d), B, ptr(bt, _i32p), bt.shape[1], ptr(sp, _i32p), n_new,
+                                                  k_new.ctypes.data, v_new.ctypes.data, src_dtype, ptr(cos, _f32p),
+                                                  ptr(sin, _f32p), rope_dim, cos.shape[0]))
 
     def paged_append(self, pool: HostPool, block_tables, start_pos, k_new, v_new):
         B, n_new = k_new.shape[0], k_new.shape[1]

@@ -741,9 +741,49 @@ static void vo_copy_row_raw(const VoPagedKV* kv, int is_v, size_t b, size_t h, s
     }
 }
 
+/* Rotary embedding of one row, runtime_inference.py:1307-1311 (and _apply_rotary,
+ * :621-636; _apply_partial_rotary, :1096-1106): pairs (i, i + half) of the first
+ * rope_dim elements, half = rope_dim / 2, become (x1*c - x2*s, x1*s + x2*c) with
+ * c = cos_row[i], s = sin_row[i], each product and sum rounded to fp32 as numpy's
+ * elementwise float32 arithmetic does; elements past rope_dim pass through. */
+void vo_rope_row(const float* x, float* out, size_t d, size_t rope_dim, const float* cos_row,
+                 const float* sin_row) {
+    const size_t half = rope_dim / 2u;
+    for (size_t i = 0; i < d; ++i) out[i] = x[i];
+    /* built with -ffp-contract=off: every product and sum is rounded separately */
+    for (size_t i = 0; i < half; ++i) {
+        out[i] = x[i] * cos_row[i] - x[i + half] * sin_row[i];
+        out[i + half] = x[i] * sin_row[i] + x[i + half] * cos_row[i];
+    }
+}
+
+static int vo_paged_append_impl(const VoPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                                uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                                const void* k_new, const void* v_new, int src_dtype,
+                                const float* rope_cos, const float* rope_sin, size_t rope_dim,
+                                size_t max_pos);
+
 int vo_paged_append(const VoPagedKV* kv, uint32_t batch, const int32_t* block_tables,
                     uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
                     const void* k_new, const void* v_new, int src_dtype) {
+    return vo_paged_append_impl(kv, batch, block_tables, max_blocks_per_seq, start_pos, n_new, k_new,
+                                v_new, src_dtype, NULL, NULL, 0, 0);
+}
+
+int vo_paged_append_rope(const VoPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                         uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                         const void* k_new, const void* v_new, int src_dtype, const float* rope_cos,
+                         const float* rope_sin, size_t rope_dim, size_t max_pos) {
+    if (!rope_cos || !rope_sin || rope_dim == 0 || rope_dim % 2u || rope_dim > kv->head_dim) return 0;
+    return vo_paged_append_impl(kv, batch, block_tables, max_blocks_per_seq, start_pos, n_new, k_new,
+                                v_new, src_dtype, rope_cos, rope_sin, rope_dim, max_pos);
+}
+
+static int vo_paged_append_impl(const VoPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                                uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                                const void* k_new, const void* v_new, int src_dtype,
+                                const float* rope_cos, const float* rope_sin, size_t rope_dim,
+                                size_t max_pos) {
     if (!vo_kv_valid(kv) || !block_tables || !start_pos || !k_new || !v_new ||
         (src_dtype != 0 && src_dtype != 1)) {
         return 0;
@@ -768,6 +808,13 @@ int vo_paged_append(const VoPagedKV* kv, uint32_t batch, const int32_t* block_ta
                 } else {
                     vo_f16_to_f32((const uint16_t*)k_new + src_off, kr, D);
                     vo_f16_to_f32((const uint16_t*)v_new + src_off, vr, D);
+                }
+                if (rope_cos) {
+                    if (t >= max_pos) { ok = 0; break; }
+                    float rot[1024];
+                    vo_rope_row(kr, rot, D, rope_dim, rope_cos + t * (rope_dim / 2u),
+                                rope_sin + t * (rope_dim / 2u));
+                    memcpy(kr, rot, D * sizeof(float));
                 }
                 vo_store_row(kv, 0, (size_t)pb, h, slot, kr);
                 vo_store_row(kv, 1, (size_t)pb, h, slot, vr);

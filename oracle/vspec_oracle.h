@@ -120,6 +120,19 @@ int vo_paged_append(const VoPagedKV* kv, uint32_t batch, const int32_t* block_ta
                     uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
                     const void* k_new, const void* v_new, int src_dtype);
 
+/* Rotary embedding of one row (runtime_inference.py:1307-1311): pairs (i, i + rope_dim/2)
+ * of the first rope_dim elements rotate by (cos_row[i], sin_row[i]) with separately
+ * rounded fp32 products and sums; the rest pass through. */
+void vo_rope_row(const float* x, float* out, size_t d, size_t rope_dim, const float* cos_row,
+                 const float* sin_row);
+
+/* vo_paged_append with K rotated first: token position t uses row t of the
+ * [max_pos][rope_dim/2] cos/sin tables (V is stored as given). */
+int vo_paged_append_rope(const VoPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                         uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                         const void* k_new, const void* v_new, int src_dtype, const float* rope_cos,
+                         const float* rope_sin, size_t rope_dim, size_t max_pos);
+
 /* Gather through the block table into per-sequence [T][H][D] (capi.c:2263-2299 order).
  * Sequences are concatenated; sequence b starts at token out_token_offset[b].
  * out_mode 0: raw pool format (f32/f16 elements; int4 codes [T][H][D/2] + scales

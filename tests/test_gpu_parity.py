@@ -369,3 +369,41 @@ def test_config5_chunk_evict_compact(oracle, gpu, mode):
     err = float(np.abs(out.cpu().numpy() - want).max())
     assert err <= TOL[DTYPE_INT4], err
     say(f"[c5] max-abs {err:.2e}")
+
+
+# ----------------------------------------------------------------------------- fused rotary + append
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+@pytest.mark.parametrize("src16", [False, True])
+@pytest.mark.parametrize("rope_frac", [1, 2])
+def test_append_rope_bitexact(oracle, gpu, dtype, src16, rope_frac):
+    """Rotary embedding fused into the append: pool bytes and the rotated q rows are
+    bit-identical to the oracle (rotate, then the plain append)."""
+    import torch
+    import vspec_rocm as vr
+    from test_oracle_pin import _rope_tables
+
+    B, H, Hq, D, P = 3, 2, 8, 128, 16
+    rope_dim = D // rope_frac
+    say(f"[rope] dtype={dtype} src16={src16} rope_dim={rope_dim}")
+    case = make_case(oracle, dtype, B, Hq, H, D, P, [40, 7, 33], seed=200 + dtype + 3 * src16 + rope_frac,
+                     num_blocks=12, src16=src16)
+    cos, sin = _rope_tables(64, rope_dim)
+    start = np.array([0, 0, 5], np.int32)
+    n_new = 7
+    kk = np.ascontiguousarray(case.k_tokens[:, :n_new])
+    vv = np.ascontiguousarray(case.v_tokens[:, :n_new])
+    assert oracle.paged_append_rope(case.host, case.tables, start, kk, vv, cos, sin, rope_dim)
+    pool = device_pool(case, gpu)
+    q = oracle.normal(301, B * n_new * Hq * D).reshape(B, n_new, Hq, D)
+    qo = vr.kv_append_rope(pool, torch.from_numpy(case.tables).to(gpu), torch.from_numpy(start).to(gpu),
+                           _np_to_dev(kk, gpu), _np_to_dev(vv, gpu), torch.from_numpy(cos).to(gpu),
+                           torch.from_numpy(sin).to(gpu), rope_dim, q=torch.from_numpy(q).to(gpu))
+    torch.cuda.synchronize()
+    assert_pools_equal(case.host, pool)
+    qg = qo.cpu().numpy()
+    for b in range(B):
+        for i in range(n_new):
+            p_ = start[b] + i
+            for h in range(Hq):
+                want = oracle.rope_row(q[b, i, h], rope_dim, cos[p_], sin[p_])
+                assert np.array_equal(qg[b, i, h].view(np.uint32), want.view(np.uint32)), (b, i, h)

@@ -424,3 +424,72 @@ def test_paged_compact_moves_blocks(oracle):
         assert np.array_equal(a[0:rows], b[5 * rows:6 * rows])
         assert np.array_equal(a[rows:2 * rows], b[6 * rows:7 * rows])
         assert np.array_equal(a[2 * rows:], b[2 * rows:])
+
+
+# ----------------------------------------------------------------------------- rotary embedding
+def _rope_tables(max_pos, rope_dim, theta=10000.0):
+    """cos/sin rows as the reference caches them (runtime_inference.py:1186-1192, 4227):
+    float32 inverse frequencies, float32 angles pos * inv_freq, float32 cos/sin."""
+    half = rope_dim // 2
+    inv = (1.0 / (theta ** (np.arange(half, dtype=np.float32) / max(1, half)))).astype(np.float32)
+    ang = np.stack([np.float32(p) * inv for p in range(max_pos)]).astype(np.float32)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def test_rope_row_special_cases(oracle):
+    D = 16
+    cos, sin = _rope_tables(40, D)
+    x = oracle.normal(71, D)
+    assert np.array_equal(oracle.rope_row(x, D, cos[0], sin[0]), x)  # position 0: identity
+    for i in range(D // 2):  # unit vectors land on (cos_i, sin_i)
+        e = np.zeros(D, np.float32)
+        e[i] = 1.0
+        out = oracle.rope_row(e, D, cos[33], sin[33])
+        want = np.zeros(D, np.float32)
+        want[i], want[i + D // 2] = cos[33][i], sin[33][i]
+        assert np.array_equal(out, want)
+    out = oracle.rope_row(x, D, cos[17], sin[17])
+    n0 = np.hypot(x[: D // 2], x[D // 2:])
+    n1 = np.hypot(out[: D // 2], out[D // 2:])
+    np.testing.assert_allclose(n1, n0, rtol=2e-6)  # rotations keep each pair's norm
+
+
+def test_rope_row_matches_float32_array_arithmetic(oracle):
+    """Bit-equal to the reference formula evaluated in numpy float32 (separately rounded
+    products and sums), including partial rotary (_apply_partial_rotary)."""
+    D = 128
+    for rope_dim in (128, 64):
+        cos, sin = _rope_tables(300, rope_dim)
+        for pos in (1, 7, 255, 299):
+            x = oracle.normal(80 + pos, D)
+            half = rope_dim // 2
+            k1, k2 = x[:half], x[half:rope_dim]
+            want = np.concatenate([k1 * cos[pos] - k2 * sin[pos], k1 * sin[pos] + k2 * cos[pos], x[rope_dim:]])
+            got = oracle.rope_row(x, rope_dim, cos[pos], sin[pos])
+            assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32)), (rope_dim, pos)
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+def test_paged_append_rope(oracle, dtype):
+    """Fused rotary + append == rotate each K row, then the plain append; V untouched."""
+    B, H, D, P, T = 2, 2, 64, 16, 21
+    cos, sin = _rope_tables(64, D)
+    bt = _tables(oracle, B, 2, 8, 9)
+    x = oracle.normal(91, B * T * H * D).reshape(B, T, H, D)
+    y = oracle.normal(92, B * T * H * D).reshape(B, T, H, D)
+    a = HostPool(dtype, 8, P, H, D)
+    b = HostPool(dtype, 8, P, H, D)
+    start = np.array([3, 11], np.int32)
+    assert oracle.paged_append_rope(a, bt, start, x, y, cos, sin, D)
+    xr = np.empty_like(x)
+    for s_ in range(B):
+        for t in range(T):
+            for h in range(H):
+                p_ = start[s_] + t
+                xr[s_, t, h] = oracle.rope_row(x[s_, t, h], D, cos[p_], sin[p_])
+    assert oracle.paged_append(b, bt, start, xr, y)
+    for u, w in zip((a.k, a.v, a.ks, a.vs), (b.k, b.v, b.ks, b.vs)):
+        if u is not None:
+            assert np.array_equal(u, w)
+    # a position past the tables fails
+    assert not oracle.paged_append_rope(HostPool(dtype, 8, P, H, D), bt, np.array([60, 0], np.int32), x, y, cos, sin, D)

@@ -363,6 +363,11 @@ struct AppendParams {
     // position token_pos[b] of block-table row token_item[b]
     const int32_t* token_item;
     const int32_t* token_pos;
+    // rotary embedding of K (rope_cos != null): rows [max_pos][rope_dim / 2]
+    const float* rope_cos;
+    const float* rope_sin;
+    uint32_t rope_dim;
+    uint32_t max_pos;
     const uint8_t* k_new;
     const uint8_t* v_new;
     uint32_t batch;
@@ -419,6 +424,35 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
 #pragma unroll
             for (int j = 0; j < EPT / 8; ++j) unpack_f16x8(s4[j], x + 8 * j);
         }
+        const bool rope = p.rope_cos != nullptr;
+        if (rope) {
+            if (pos >= p.max_pos) continue;  // no table row: the token is not written
+            if (!which) {
+#pragma clang fp contract(off)
+                // pairs (i, i + half) of the first rope_dim elements rotate by row `pos`:
+                // x1*c - x2*s, x1*s + x2*c, each product and sum rounded separately (no
+                // fused multiply-add: hipcc contracts by default)
+                const uint32_t half = p.rope_dim / 2;
+                const size_t row0 = src_el - e0;  // element 0 of this token-head row
+                const float* cr = p.rope_cos + (size_t)pos * half;
+                const float* sr = p.rope_sin + (size_t)pos * half;
+#pragma unroll
+                for (int e = 0; e < EPT; ++e) {
+                    const uint32_t d = (uint32_t)e0 + e;
+                    if (d >= p.rope_dim) continue;
+                    const uint32_t i = d < half ? d : d - half;
+                    const size_t pe = row0 + (d < half ? d + half : d - half);
+                    float other;
+                    if constexpr (SRC == VSPEC_KV_F32) {
+                        other = reinterpret_cast<const float*>(src)[pe];
+                    } else {
+                        other = half_bits_to_float(reinterpret_cast<const uint16_t*>(src)[pe]);
+                    }
+                    const float c = cr[i], sn = sr[i];
+                    x[e] = d < half ? x[e] * c - other * sn : other * sn + x[e] * c;
+                }
+            }
+        }
 
         uint8_t* dst = which ? p.v : p.k;
         if constexpr (DT == VSPEC_KV_F32) {
@@ -427,7 +461,7 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
             d4[1] = make_float4(x[4], x[5], x[6], x[7]);
         } else if constexpr (DT == VSPEC_KV_F16) {
             uint32_t hb[8];
-            if constexpr (SRC == VSPEC_KV_F16) {
+            if (SRC == VSPEC_KV_F16 && !(rope && !which)) {
                 // pure copy of the source bits
                 const uint4 w = *reinterpret_cast<const uint4*>(src + src_el * 2);
                 const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
@@ -498,6 +532,42 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
                 p.ks[int4_ks_index(bh, p.head_dim / 32, p.block_tokens, slot, c)] = (uint16_t)s16;
             }
         }
+    }
+}
+
+// Rotary embedding of the query rows of the appended tokens: q [B][n_new][Hq][D] fp32,
+// token (b, i) at position start_pos[b] + i; tokens without a table row are not written.
+struct RopeQParams {
+    const float* q_in;
+    float* q_out;
+    const int32_t* start_pos;
+    const float* rope_cos;
+    const float* rope_sin;
+    uint32_t batch, n_new, hq, head_dim, rope_dim, max_pos;
+};
+
+__global__ __launch_bounds__(256) void rope_q(RopeQParams p) {
+    const uint64_t total = (uint64_t)p.batch * p.n_new * p.hq * p.head_dim;
+    for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
+         it += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t d = (uint32_t)(it % p.head_dim);
+        const uint64_t row = it / p.head_dim;  // ((b * n_new + i) * hq + h)
+        const uint32_t i = (uint32_t)((row / p.hq) % p.n_new);
+        const uint32_t b = (uint32_t)(row / ((uint64_t)p.hq * p.n_new));
+        const int32_t sp = p.start_pos[b];
+        if (sp < 0) continue;
+        const uint32_t pos = (uint32_t)sp + i;
+        if (pos >= p.max_pos) continue;
+        const float* x = p.q_in + row * p.head_dim;
+        float y = x[d];
+        if (d < p.rope_dim) {
+#pragma clang fp contract(off)
+            const uint32_t half = p.rope_dim / 2;
+            const uint32_t k = d < half ? d : d - half;
+            const float c = p.rope_cos[(size_t)pos * half + k], sn = p.rope_sin[(size_t)pos * half + k];
+            y = d < half ? x[d] * c - x[d + half] * sn : x[d - half] * sn + x[d] * c;
+        }
+        p.q_out[row * p.head_dim + d] = y;
     }
 }
 
@@ -1007,6 +1077,54 @@ int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* 
     p.n_new = n_new;
     p.max_blocks = max_blocks_per_seq;
     return append_launch("kv_append launch", kv, p, src_dtype, stream);
+}
+
+int vspec_rocm_kv_append_rope(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
+                              uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,
+                              const void* k_new, const void* v_new, int32_t src_dtype, const float* rope_cos,
+                              const float* rope_sin, uint32_t rope_dim, uint32_t max_pos, const float* q_in,
+                              float* q_out, uint32_t num_q_heads, void* stream) {
+    if (!check_kv(kv, "kv_append_rope")) return 0;
+    if (src_dtype != VSPEC_KV_F32 && src_dtype != VSPEC_KV_F16) {
+        set_err("kv_append_rope: src_dtype must be f32 or f16");
+        return 0;
+    }
+    if (!rope_cos || !rope_sin || rope_dim == 0 || rope_dim % 2 != 0 || rope_dim > kv->head_dim || max_pos == 0) {
+        set_err("kv_append_rope: need cos/sin tables and an even rope_dim <= head_dim");
+        return 0;
+    }
+    if ((q_in == nullptr) != (q_out == nullptr) || (q_in && num_q_heads == 0)) {
+        set_err("kv_append_rope: q_in and q_out go together, with num_q_heads > 0");
+        return 0;
+    }
+    if (batch == 0 || n_new == 0) return 1;
+    if (!block_tables || !start_pos || !k_new || !v_new || max_blocks_per_seq == 0) {
+        set_err("kv_append_rope: null argument");
+        return 0;
+    }
+    AppendParams p = {};
+    p.block_tables = block_tables;
+    p.start_pos = start_pos;
+    p.k_new = (const uint8_t*)k_new;
+    p.v_new = (const uint8_t*)v_new;
+    p.batch = batch;
+    p.n_new = n_new;
+    p.max_blocks = max_blocks_per_seq;
+    p.rope_cos = rope_cos;
+    p.rope_sin = rope_sin;
+    p.rope_dim = rope_dim;
+    p.max_pos = max_pos;
+    if (!append_launch("kv_append_rope launch", kv, p, src_dtype, stream)) return 0;
+    if (q_in) {
+        RopeQParams rq = {q_in, q_out, start_pos, rope_cos, rope_sin, batch, n_new, num_q_heads,
+                          kv->head_dim, rope_dim, max_pos};
+        const uint64_t total = (uint64_t)batch * n_new * num_q_heads * kv->head_dim;
+        uint64_t blocks = (total + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        hipLaunchKernelGGL(rope_q, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, rq);
+        HIP_CHECK(hipGetLastError(), "rope_q launch");
+    }
+    return 1;
 }
 
 int vspec_rocm_kv_append_tokens(const VspecPagedKV* kv, uint32_t n_tokens, const int32_t* token_item,

@@ -147,6 +147,9 @@ SIGNATURES = {
     "vspec_rocm_kv_pool_create": (C.c_int, [C.POINTER(VspecPagedKV), C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
     "vspec_rocm_kv_pool_destroy": (None, [C.POINTER(VspecPagedKV)]),
     "vspec_rocm_kv_append": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, C.c_uint32, _vp, C.c_uint32, _vp, _vp, C.c_int32, _vp]),
+    "vspec_rocm_kv_append_rope": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, C.c_uint32, _vp, C.c_uint32, _vp,
+                                            _vp, C.c_int32, _vp, _vp, C.c_uint32, C.c_uint32, _vp, _vp, C.c_uint32,
+                                            _vp]),
     "vspec_rocm_kv_gather": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, C.c_uint32, _vp, C.c_uint32, _vp, C.c_int32, _vp, _vp, _vp, _vp, _vp]),
     "vspec_rocm_kv_compact": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp]),
     "vspec_rocm_paged_decode_workspace_bytes": (C.c_size_t, [C.POINTER(VspecPagedAttnDesc)]),
@@ -277,6 +280,35 @@ def kv_append(pool: PagedPool, block_tables, start_pos, k_new, v_new, stream=Non
     d = pool.desc()
     _check(lib().vspec_rocm_kv_append(C.byref(d), B, bt.data_ptr(), bt.shape[1], sp.data_ptr(), n_new,
                                       k_new.data_ptr(), v_new.data_ptr(), src, _stream(stream)), "kv_append")
+
+
+def kv_append_rope(pool, block_tables, start_pos, k_new, v_new, rope_cos, rope_sin, rope_dim=None, q=None,
+                   stream=None):
+    """vspec_rocm_kv_append_rope: kv_append with K (and q [B][n_new][Hq][D] fp32, when
+    given) rotated by rows start_pos + i of rope_cos / rope_sin [max_pos][rope_dim/2]
+    (fp32, device).  Returns the rotated q (or None)."""
+    import torch
+
+    B, n_new = k_new.shape[0], k_new.shape[1]
+    assert k_new.is_contiguous() and v_new.is_contiguous()
+    assert rope_cos.dtype == torch.float32 and rope_cos.is_contiguous() and rope_sin.is_contiguous()
+    src = KV_F16 if k_new.dtype == torch.float16 else KV_F32
+    rope_dim = int(rope_dim if rope_dim is not None else 2 * rope_cos.shape[1])
+    bt = block_tables.to(torch.int32).contiguous()
+    sp = start_pos.to(torch.int32).contiguous()
+    q_out = None
+    qin = qout = None
+    hq = 0
+    if q is not None:
+        assert q.dtype == torch.float32 and q.is_contiguous()
+        q_out = torch.empty_like(q)
+        qin, qout, hq = q.data_ptr(), q_out.data_ptr(), q.shape[2]
+    kv = pool.desc()
+    _check(lib().vspec_rocm_kv_append_rope(C.byref(kv), B, bt.data_ptr(), bt.shape[1], sp.data_ptr(), n_new,
+                                           k_new.data_ptr(), v_new.data_ptr(), src, rope_cos.data_ptr(),
+                                           rope_sin.data_ptr(), rope_dim, rope_cos.shape[0], qin, qout, hq,
+                                           _stream(stream)), "kv_append_rope")
+    return q_out
 
 
 def kv_append_tokens(pool, token_item, token_pos, block_tables, k_new, v_new, stream=None):
