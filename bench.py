@@ -142,6 +142,20 @@ def load_traffic(workload):
         return None
 
 
+def calibration_copy(args, dev):
+    """One device-to-device copy of a known size (--calibration-copy-mib): rocprofv3
+    FETCH_SIZE / WRITE_SIZE of this copy scale the counters to bytes."""
+    if args.calibration_copy_mib <= 0:
+        return
+    import torch
+
+    src = torch.empty(args.calibration_copy_mib << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def run_c5(args, wl, kv_dtype, mode):
     """Config 5: 8 sequences with int4 contexts L0 ~ U[16384, 32256] (seeded) each append a
     512-token fp16 chunk through quantize-on-write, evict the oldest 25 % of their blocks,
@@ -220,6 +234,7 @@ def run_c5(args, wl, kv_dtype, mode):
         if e:
             e[3].record()
 
+    calibration_copy(args, dev)
     for _ in range(args.warmup):
         flow(None)
     torch.cuda.synchronize()
@@ -250,7 +265,8 @@ def run_c5(args, wl, kv_dtype, mode):
         },
         "roofline": {"bound": "hbm", "achieved": gbs(decode_bytes, stage[2]), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": gbs(decode_bytes, stage[2]) / PEAK_GBS, "traffic": load_traffic(args.workload),
-                     "kernel": "decode_partial (int4)", "algorithmic_bytes_per_launch": decode_bytes},
+                     "kernel": "decode_mfma_i4" + (" + decode_combine" if vr.decode_workspace_bytes(desc) else ""),
+                     "algorithmic_bytes_per_launch": decode_bytes},
     }
 
 
@@ -265,6 +281,9 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="copy a buffer of this many MiB on the device once before warm-up, so that "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE of the same run can be scaled to bytes")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -359,6 +378,7 @@ def main():
         if ev:
             ev[1].record()
 
+    calibration_copy(args, dev)
     evs = [None] * 0
     for i in range(args.warmup):
         step(-1 - i)
@@ -399,7 +419,7 @@ def main():
                            "p10_ms": attn_ms[len(attn_ms) // 10], "p90_ms": attn_ms[(9 * len(attn_ms)) // 10]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": traffic,
-                     "kernel": ("decode_mfma_f16" if wl["dtype"] == "f16" else "decode_partial")
+                     "kernel": {"f16": "decode_mfma_f16", "int4": "decode_mfma_i4", "f32": "decode_partial"}[wl["dtype"]]
                                + (" + decode_combine" if ws_bytes else ""),
                      "algorithmic_bytes_per_launch": alg},
     }
