@@ -407,3 +407,88 @@ def test_append_rope_bitexact(oracle, gpu, dtype, src16, rope_frac):
             for h in range(Hq):
                 want = oracle.rope_row(q[b, i, h], rope_dim, cos[p_], sin[p_])
                 assert np.array_equal(qg[b, i, h].view(np.uint32), want.view(np.uint32)), (b, i, h)
+
+
+# ----------------------------------------------------------------------------- registry entry
+def _legacy_launch(q, k, v, mode):
+    """vspec_make_rocm_backend().launch_attention with the reference's context convention
+    (cpu_backend.c:40-51): input = host q [H][D], weight = VspecKVCache* over host
+    [T][H][D] fp32 rows, output = host out; numerics from the same env switch."""
+    import ctypes as C
+    import os
+    import vspec_rocm as vr
+
+    T, H, D = k.shape
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.full((H, D), 7.0, np.float32)
+    cache = vr.VspecKVCache()
+    cache.key, cache.value = k.ctypes.data, v.ctypes.data
+    cache.max_tokens, cache.num_heads, cache.head_dim, cache.current_tokens = T, H, D, T
+    ctx = vr.VspecKernelContext()
+    ctx.input, ctx.weight, ctx.output = q.ctypes.data, C.cast(C.pointer(cache), C.c_void_p), out.ctypes.data
+    if mode:
+        os.environ["VSPEC_3BIT_RUNTIME_MODULE"] = "1"
+    else:
+        os.environ.pop("VSPEC_3BIT_RUNTIME_MODULE", None)
+    os.environ.pop("VSPEC_FUSED_BITS", None)
+    be = vr.backend()
+    be.launch_attention(C.byref(ctx))
+    err = vr.last_error()
+    return out, err
+
+
+def test_backend_attention_demo_known_answer(gpu):
+    """examples/attention_demo.c through the ROCm registry entry (2 heads, D=4, 2 tokens):
+    the demo's printed values, both numerics modes."""
+    k0 = [0.2, 0.1, 0.0, -0.1, 0.1, 0.3, -0.2, 0.4]
+    v0 = [0.5, 0.0, 0.1, 0.0, 0.2, 0.3, 0.1, -0.2]
+    k1 = [0.0, 0.2, 0.1, 0.3, -0.1, 0.2, 0.2, 0.1]
+    v1 = [0.1, 0.2, 0.4, 0.2, 0.0, 0.1, 0.3, 0.2]
+    q = np.array([0.3, 0.1, -0.1, 0.0, 0.2, -0.2, 0.3, 0.1], np.float32).reshape(2, 4)
+    k = np.array([k0, k1], np.float32).reshape(2, 2, 4)
+    v = np.array([v0, v1], np.float32).reshape(2, 2, 4)
+    want = np.array([[0.3030, 0.0985, 0.2478, 0.0985], [0.0983, 0.1983, 0.2017, 0.0035]])
+    for mode in (0, 1):
+        out, err = _legacy_launch(q, k, v, mode)
+        assert np.array_equal(np.round(out.astype(np.float64), 4), want), (mode, out, err)
+
+
+@pytest.mark.parametrize("D", [4, 64, 96, 128])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_backend_legacy_context_matches_oracle(oracle, gpu, D, mode):
+    """Any head size through the legacy context path, fp32 KV, against the oracle's
+    attention_ref (1e-4), including keys and queries that make the clamps fire."""
+    H, T = 3, 150
+    q = oracle.normal(400 + D, H * D).reshape(H, D) * 3
+    k = oracle.normal(401 + D, T * H * D).reshape(T, H, D)
+    v = oracle.normal(402 + D, T * H * D).reshape(T, H, D)
+    k = k.copy()
+    k[::9, 1, 0] = 30.0
+    out, err = _legacy_launch(q, k, v, mode)
+    want = oracle.attention_ref(mode, q, k, v)
+    assert np.abs(out - want).max() <= 1e-4, (np.abs(out - want).max(), err)
+
+
+def test_backend_paged_flag(oracle, gpu):
+    """launch_attention with VSPEC_KCTX_FLAG_PAGED takes a VspecPagedAttnDesc of device
+    pointers and equals vspec_rocm_paged_decode_attention."""
+    import ctypes as C
+    import torch
+    import vspec_rocm as vr
+
+    case = make_case(oracle, DTYPE_F16, 3, 8, 2, 128, 16, [40, 75, 9], seed=44)
+    pool = build_both(oracle, case, gpu)
+    tab = torch.from_numpy(case.tables).to(gpu)
+    ctx_t = torch.from_numpy(case.ctx).to(gpu)
+    q = torch.from_numpy(case.q).to(gpu)
+    want = vr.paged_decode(pool, tab, ctx_t, q, numerics=1)
+    out = torch.zeros_like(q)
+    d = vr.make_decode_desc(pool, tab, ctx_t, q, out, case.tmax, numerics=1)
+    kc = vr.VspecKernelContext()
+    kc.weight = C.cast(C.pointer(d), C.c_void_p)
+    kc.config.flags = vr.KCTX_FLAG_PAGED
+    vr.backend().launch_attention(C.byref(kc))
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
