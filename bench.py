@@ -265,7 +265,7 @@ def run_c5(args, wl, kv_dtype, mode):
         },
         "roofline": {"bound": "hbm", "achieved": gbs(decode_bytes, stage[2]), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": gbs(decode_bytes, stage[2]) / PEAK_GBS, "traffic": load_traffic(args.workload),
-                     "kernel": "decode_mfma_i4" + (" + decode_combine" if vr.decode_workspace_bytes(desc) else ""),
+                     "kernel": "decode_mfma_i4",
                      "algorithmic_bytes_per_launch": decode_bytes},
     }
 
@@ -419,8 +419,8 @@ def main():
                            "p10_ms": attn_ms[len(attn_ms) // 10], "p90_ms": attn_ms[(9 * len(attn_ms)) // 10]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": traffic,
-                     "kernel": {"f16": "decode_mfma_f16", "int4": "decode_mfma_i4", "f32": "decode_partial"}[wl["dtype"]]
-                               + (" + decode_combine" if ws_bytes else ""),
+                     "kernel": {"f16": "decode_mfma_f16", "int4": "decode_mfma_i4",
+                                "f32": "decode_partial" + (" + decode_combine" if ws_bytes else "")}[wl["dtype"]],
                      "algorithmic_bytes_per_launch": alg},
     }
     if not args.no_cpu_baseline:

@@ -36,16 +36,31 @@ struct Frags {
 
 // PB: block_tokens known at compile time (16), or 0 for any multiple of 16;
 // NB: tiles in flight per wave
+//
+// Schedule: the workgroup takes the tile range [lo, hi) of the work split (it may start
+// and end inside work items and span several); wave w streams the range's tiles
+// lo + w, lo + w + 4, ... through its ring of NB tile buffers without stopping at work
+// item boundaries: the ring's loads run NB tiles ahead on their own cursor, and where
+// the processed tiles enter a new work item the wave hands its softmax state for the
+// old one to an LDS merge slot, resets it and prepares the new item's q operands from
+// q rows staged in LDS up front.  The last of the four waves to hand in an item's state
+// merges the four; no barrier stops the ring.
 template <int D, int GW, int PB, int NB>
 __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
-    constexpr int NQK = D / 32;  // QK MFMAs per tile (each on 32 d)
-    constexpr int NDT = D / 16;  // PV d-tiles
-    __shared__ float qs[GW][D];
-    // QK B operands per lane (hi, lo for each 32-wide d chunk), read back every tile
-    __shared__ uint4 qb_lds[NQK][2][64];
-    __shared__ float comb[kWaves][GW][D + 2];
+    constexpr int NQK = D / 32;   // QK MFMAs per tile (each on 32 d)
+    constexpr int NDT = D / 16;   // PV d-tiles
+    constexpr int kQStage = 4;    // item segments whose q rows are staged up front
+    constexpr int kSlots = 2;     // item segments being merged at once
+    __shared__ float qraw[kQStage][GW][D];
+    __shared__ float qs[kWaves][GW][D];  // per wave: q' of its current item
+    // per wave: QK B operands (hi, lo for each 32-wide d chunk), read back every tile
+    __shared__ uint4 qb_lds[kWaves][NQK][2][64];
+    __shared__ float comb[kSlots][kWaves][GW][D + 2];
     __shared__ float patch_val[kWaves][kTile][4];
     __shared__ int patch_flag[kWaves][kTile];
+    __shared__ int slot_cnt[kSlots];
+    __shared__ int slot_seg[kSlots];
+    __shared__ SplitShared split_sh;
 
     const int lane = threadIdx.x & 63;
     // wave index as a scalar: tile loop control and block-table reads stay on the
@@ -53,76 +68,101 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4;   // row group
     const int n = lane & 15;   // column / token within the tile
-    const int part = blockIdx.x;
-    const int b = blockIdx.z;
-    const int hk = blockIdx.y / p.gsplit;
-    const int hq0 = hk * (p.gsplit * GW) + (blockIdx.y % p.gsplit) * GW;
 
-    const int ctx = min(max(p.ctx_lens[b], 0), (int)(p.max_blocks * p.block_tokens));
-    const int ntiles = min((ctx + kTile - 1) / kTile, (int)(p.max_parts * p.tiles_per_part));
-    const int nparts = max(1, (ntiles + (int)p.tiles_per_part - 1) / (int)p.tiles_per_part);
-    if (part >= nparts) return;
-    const int tile_begin = part * (int)p.tiles_per_part;
-    const int tile_end = min(ntiles, tile_begin + (int)p.tiles_per_part);
+    const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
+    const WorkSplit ws = work_split(p, ips, split_sh);
+    if (ws.lo >= ws.hi) return;
+    const ItemCursor first = cursor_at(p, ws);
 
-    // ---- q' = clip(q) * scale * log2(e): wave w prepares head w ----
-    if (wave < GW) {
-        const float* qrow = p.q + ((size_t)b * p.hq + hq0 + wave) * D;
-        constexpr int E = D / 64;
-        float x[E];
-        float s = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            x[e] = qrow[lane * E + e];
-            s += x[e];
+    // q rows of the first kQStage segments (rows GW*y .. GW*y + GW - 1 of sequence b are
+    // contiguous); merge slot s serves segment s first
+    {
+        ItemCursor c = first;
+        for (int s = 0; s < kQStage; ++s) {
+            const float* qrow = p.q + ((size_t)c.b * p.hq + (size_t)c.y * GW) * D;
+            for (int i = threadIdx.x; i < GW * D; i += kWaves * 64) qraw[s][i / D][i % D] = qrow[i];
+            if (c.item0 + c.U >= ws.hi) break;
+            cursor_next(p, ips, c);
         }
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
-        const float mean = s * (1.0f / D);
-        float v = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) v = fmaf(x[e] - mean, x[e] - mean, v);
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
-        const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v * (1.0f / D))), p.input_clip);
-#pragma unroll
-        for (int e = 0; e < E; ++e) qs[wave][lane * E + e] = fminf(fmaxf(x[e], -th), th) * p.qscale;
+        if (threadIdx.x < kSlots) {
+            slot_cnt[threadIdx.x] = 0;
+            slot_seg[threadIdx.x] = threadIdx.x;
+        }
     }
     __syncthreads();
 
-    // B operands of the QK MFMAs: column n < GW holds head n, split hi + lo
-    if (wave == 0) {
+    // ---- q' = clip(q) * scale * log2(e) of work item c (segment s) for this wave, and
+    // the B operands of the QK MFMAs: column n < GW holds head n, split hi + lo ----
+    auto qprep = [&](const int s, const ItemCursor& c) {
+        constexpr int E = D / 64;
+        if (s >= kQStage) {
+            // rows past the staged ones go through this wave's qs first, so that only this
+            // rare branch waits for a global load (the other path keeps the ring's loads
+            // in flight)
+#pragma unroll
+            for (int h = 0; h < GW; ++h) {
+                const float* qrow = p.q + ((size_t)c.b * p.hq + (size_t)c.y * GW + h) * D;
+#pragma unroll
+                for (int e = 0; e < E; ++e) qs[wave][h][lane * E + e] = qrow[lane * E + e];
+            }
+        }
+        float (*src)[D] = s < kQStage ? qraw[s] : qs[wave];
+#pragma unroll
+        for (int h = 0; h < GW; ++h) {
+            float x[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[e] = src[h][lane * E + e];
+            float sm = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) sm += x[e];
+            const float mean = wave_sum(sm) * (1.0f / D);
+            float v = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) v = fmaf(x[e] - mean, x[e] - mean, v);
+            v = wave_sum(v);
+            const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v * (1.0f / D))), p.input_clip);
+#pragma unroll
+            for (int e = 0; e < E; ++e) qs[wave][h][lane * E + e] = fminf(fmaxf(x[e], -th), th) * p.qscale;
+        }
+        // this wave's own LDS writes are read back below: a wave's LDS accesses complete
+        // in program order
 #pragma unroll
         for (int i = 0; i < NQK; ++i) {
             h8_t hi8, lo8;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float qv = n < GW ? qs[n < GW ? n : 0][32 * i + 8 * g + j] : 0.f;
+                const float qv = n < GW ? qs[wave][n < GW ? n : 0][32 * i + 8 * g + j] : 0.f;
                 const _Float16 hi = (_Float16)qv;
                 hi8[j] = hi;
                 lo8[j] = (_Float16)(qv - (float)hi);
             }
-            qb_lds[i][0][lane] = __builtin_bit_cast(uint4, hi8);
-            qb_lds[i][1][lane] = __builtin_bit_cast(uint4, lo8);
+            qb_lds[wave][i][0][lane] = __builtin_bit_cast(uint4, hi8);
+            qb_lds[wave][i][1][lane] = __builtin_bit_cast(uint4, lo8);
         }
-    }
-    __syncthreads();
+    };
 
     const int P = PB ? PB : (int)p.block_tokens;
     const int tiles_per_block = P / kTile;
-    const int32_t* table = p.block_tables + (size_t)b * p.max_blocks;
     const _Float16* kbase = reinterpret_cast<const _Float16*>(p.k);
     const _Float16* vbase = reinterpret_cast<const _Float16*>(p.v);
+    const int ctx_cap = (int)(p.max_blocks * p.block_tokens);
 
     // Loads are issued unconditionally (a tile past the range or behind an invalid
     // table entry reads block 0 and reports false): with no branches around them the
     // compiler counts outstanding loads exactly and waits only for the tile it needs.
-    auto load = [&](int tile, Frags<D>& f) -> bool {
-        tile = __builtin_amdgcn_readfirstlane(tile);
-        const bool in_range = tile < tile_end;
-        const int entry = table[(in_range ? tile : tile_end - 1) / tiles_per_block];
+    // `lc` is the work item of the tiles being loaded (it runs NB tiles ahead).
+    ItemCursor lc = first;
+    auto load = [&](int t, Frags<D>& f) -> bool {
+        t = __builtin_amdgcn_readfirstlane(t);
+        const bool in_range = t < ws.hi;
+        if (in_range) {
+            while (t >= lc.item0 + lc.U) cursor_next(p, ips, lc);
+        }
+        const int tile = in_range ? t - lc.item0 : 0;
+        const const_i32* table = as_const(p.block_tables) + (size_t)lc.b * p.max_blocks;
+        const int entry = table[tile / tiles_per_block];
         const bool ok = in_range && entry >= 0 && (uint32_t)entry < p.num_blocks;
-        const size_t tidx = (size_t)(ok ? entry : 0) * p.hkv + hk;
+        const size_t tidx = (size_t)(ok ? entry : 0) * p.hkv + lc.y / (int)p.gsplit;
         const int slot0 = (tile % tiles_per_block) * kTile;
         const uint4* kr = reinterpret_cast<const uint4*>(kbase + (tidx * P + slot0 + n) * D + 8 * g);
 #pragma unroll
@@ -134,12 +174,16 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     };
 
     f4_t acc[NDT];
-#pragma unroll
-    for (int j = 0; j < NDT; ++j) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
     // running max starts finite so exp2(s - m_run) is 0, never NaN, in the columns
     // that hold no head (their scores stay -inf)
-    float m_run = -1e30f;
-    float l_run = 0.f;  // sum of p for head n over this lane's tokens
+    float m_run;
+    float l_run;  // sum of p for head n over this lane's tokens
+    auto reset = [&]() {
+#pragma unroll
+        for (int j = 0; j < NDT; ++j) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
+        m_run = -1e30f;
+        l_run = 0.f;
+    };
     // score clip per lane: columns that hold no head clip to -inf (3-bit mode: +-24*log2e)
     const float clip_hi = n < GW ? p.logit_clip : -INFINITY;
     const float clip_lo = n < GW ? -p.logit_clip : -INFINITY;
@@ -186,8 +230,8 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < NQK; ++i) {
-            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[i][0][lane]), sh, 0, 0, 0);
-            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[i][1][lane]), sl, 0, 0, 0);
+            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[wave][i][0][lane]), sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[wave][i][1][lane]), sl, 0, 0, 0);
         }
         return sh + sl;
     };
@@ -216,7 +260,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float x = half_bits_to_float((w4[e / 2] >> (16 * (e % 2))) & 0xffffu);
-                    a = fmaf(qs[h][32 * i + 8 * g + e], fminf(fmaxf(x, -th), th), a);
+                    a = fmaf(qs[wave][h][32 * i + 8 * g + e], fminf(fmaxf(x, -th), th), a);
                 }
             }
             part[h] = add_rows(a);
@@ -256,7 +300,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
 
     // one tile; a tile that is out of range or behind an invalid table entry has no
     // valid keys and contributes nothing
-    auto process = [&](Frags<D>& f, const bool ok, const int tile) {
+    auto process = [&](Frags<D>& f, const bool ok, const int tile, const int ctx) {
         const int nvalid = ok ? min(kTile, ctx - tile * kTile) : 0;
         const Screen sn = screen(f, nvalid);
         f4_t sc = qk(f);
@@ -304,13 +348,57 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         }
     };
 
-    // NB tiles in flight per wave: buffer u holds tile t0 + (k + u) * kWaves and is
-    // reloaded with the tile NB steps ahead right after it is processed.  The trip
-    // count is uniform (rounded up to NB; the extra tiles are out of range and fully
+    // Hand this wave's state for segment s (work item c) to merge slot s % kSlots; the
+    // last of the kWaves waves to hand in merges the four states.  A slot serves segment
+    // s once segment s - kSlots is merged; waves hand in segments in order, so the wave
+    // furthest behind never waits here and every wait ends.
+    auto arrive = [&](const int s, const ItemCursor& c) {
+        const int slot = s % kSlots;
+        while (__hip_atomic_load(&slot_seg[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != s)
+            __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        const float l = add_rows(l_run);
+        if (n < GW) {
+#pragma unroll
+            for (int j = 0; j < NDT; ++j) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) comb[slot][wave][n][2 + 16 * j + 4 * g + r] = acc[j][r];
+            }
+            if (g == 0) {
+                comb[slot][wave][n][0] = m_run;
+                comb[slot][wave][n][1] = l;
+            }
+        }
+        // LDS-only fences: the merge order needs no wait for the ring's global loads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        int before = 0;
+        if (lane == 0) before = __hip_atomic_fetch_add(&slot_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        before = __builtin_amdgcn_readfirstlane(before);
+        if (before == kWaves - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            const bool whole = c.item0 >= ws.lo && c.item0 + c.U <= ws.hi;
+            merge_segment<D, GW>(p, comb[slot], lane, (size_t)c.b * p.hq + (size_t)c.y * GW, whole, s == 0 ? 0 : 1);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            if (lane == 0) {
+                slot_cnt[slot] = 0;
+                __hip_atomic_store(&slot_seg[slot], s + kSlots, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+    };
+
+    // NB tiles in flight per wave: buffer u holds the wave's tile k + u and is reloaded
+    // with the tile NB steps ahead right after it is processed.  The trip count is
+    // uniform per wave (rounded up to NB; the extra tiles are out of range and fully
     // masked) and every step loads and processes unconditionally, so the compiler's
     // wait counts stay exact.
-    const int t0 = tile_begin + wave;
-    const int nt = t0 < tile_end ? (tile_end - t0 + kWaves - 1) / kWaves : 0;
+    ItemCursor pc = first;  // work item of the tiles being processed
+    int seg = 0;            // its segment index in this workgroup
+    int pctx = min(max(as_const(p.ctx_lens)[pc.b], 0), ctx_cap);
+    reset();
+    qprep(0, pc);
+    const int len = ws.hi - ws.lo;
+    const int t0 = ws.lo + wave;
+    const int nt = wave < len ? (len - wave + kWaves - 1) / kWaves : 0;
     Frags<D> f[NB];
     bool ok[NB];
 #pragma unroll
@@ -319,26 +407,29 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             const int t = t0 + (k + u) * kWaves;
-            process(f[u], ok[u], t);
+            if (t < ws.hi && t >= pc.item0 + pc.U) {
+                do {
+                    arrive(seg, pc);
+                    ++seg;
+                    cursor_next(p, ips, pc);
+                    reset();
+                } while (t >= pc.item0 + pc.U);
+                pctx = min(max(as_const(p.ctx_lens)[pc.b], 0), ctx_cap);
+                qprep(seg, pc);
+            }
+            process(f[u], ok[u], t - pc.item0, pctx);
             ok[u] = load(t + NB * kWaves, f[u]);
         }
     }
-
-    // ---- wave result: column n < GW holds head n; lane (g, n) has d = 16j + 4g + r ----
-    l_run = add_rows(l_run);
-    if (n < GW) {
-#pragma unroll
-        for (int j = 0; j < NDT; ++j) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) comb[wave][n][2 + 16 * j + 4 * g + r] = acc[j][r];
-        }
-        if (g == 0) {
-            comb[wave][n][0] = m_run;
-            comb[wave][n][1] = l_run;
-        }
+    // hand in the current segment and every later one of the workgroup (empty states)
+    while (true) {
+        arrive(seg, pc);
+        if (pc.item0 + pc.U >= ws.hi) break;
+        ++seg;
+        cursor_next(p, ips, pc);
+        reset();
     }
-    __syncthreads();
-    merge_waves<D, GW>(p, comb, b, hq0, part, nparts);
+    arrive_partials<D, GW>(p, ws, split_sh, ips, first, pc);
 }
 
 #ifndef VSPEC_F16_TILES_IN_FLIGHT

@@ -146,6 +146,9 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// full-wave sum (every lane gets it)
+__device__ __forceinline__ float wave_sum(float x) { return add_rows(group_sum<16>(x)); }
+
 // Max over the 64/N groups of a wave when x is uniform inside each aligned group of N.
 template <int N>
 __device__ __forceinline__ float max_across_groups(float x) {
@@ -182,6 +185,12 @@ struct DecodeParams {
     float alpha;       // std-clamp alpha
     float logit_clip;  // +-24*log2(e) in 3-bit mode, +inf otherwise
     float input_clip;  // 16 in 3-bit mode, +inf otherwise
+    // split of the MFMA kernels (see WorkSplit): part_ml / part_acc then hold two
+    // partial slots per workgroup, [grid][2][GW][2] and [grid][2][GW][D]
+    uint32_t* arrivals;    // [batch * hkv * gsplit]; zero between launches
+    uint32_t batch;
+    uint32_t max_tiles;    // tiles of the host's context bound (max_ctx_len)
+    uint32_t chunk_tiles;  // tiles per workgroup, or 0: split evenly over gridDim.x
 };
 
 
@@ -225,6 +234,331 @@ __device__ __forceinline__ void merge_waves(const DecodeParams& p, const float (
                 p.part_ml[2 * slot + 1] = l;
             }
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Work split of the MFMA decode kernels.
+//
+// A work item is (sequence b, kv head, group of GW query heads); it has
+// U_b = max(1, min(ceil(ctx_b / 16), max_tiles)) tiles.  The tiles of all work items
+// are laid end to end, sequence-major in ctx_lens order with the hkv * gsplit items of
+// a sequence adjacent, T tiles in all.  Workgroup g takes the tiles [lo_g, lo_{g+1}):
+//   balanced  lo_g = floor(g * T / G), G = min(gridDim.x, T)
+//   chunked   lo_g = g * chunk_tiles
+// so every workgroup streams the same number of tiles whatever the context lengths.
+// A work item that lies inside one workgroup's range goes straight to the output; one
+// that spans several leaves one partial (max, sum, acc) per workgroup, in slot 0 when
+// it is that workgroup's first segment and slot 1 when its last, and the workgroup that
+// arrives last at the item's counter merges them and resets the counter.  No
+// workgroup ever waits for another.
+// ---------------------------------------------------------------------------
+// Block tables and context lengths do not change while a decode kernel runs.  Read
+// through the constant address space, their wave-uniform reads stay scalar loads even
+// in loops that also store to global memory (the compiler cannot otherwise prove that
+// those stores leave them untouched).
+typedef const __attribute__((address_space(4))) int32_t const_i32;
+__device__ __forceinline__ const const_i32* as_const(const int32_t* ptr) { return (const const_i32*)ptr; }
+
+struct WorkSplit {
+    int total;   // T
+    int groups;  // G (balanced split), 0 for the chunked split
+    int lo, hi;  // this workgroup's tiles
+    int b;       // sequence holding tile lo
+    int seq0;    // index of that sequence's first tile
+};
+
+struct SplitShared {
+    int wsum[kWaves];
+    int b;
+    int seq0;
+    int last;
+};
+
+__device__ __forceinline__ int item_tiles(const DecodeParams& p, int b) {
+    const int ctx = min(max(as_const(p.ctx_lens)[b], 0), (int)(p.max_blocks * p.block_tokens));
+    return max(1, min((ctx + kTile - 1) / kTile, (int)p.max_tiles));
+}
+
+// first tile of workgroup g
+__device__ __forceinline__ int split_lo(const DecodeParams& p, const WorkSplit& w, int g) {
+    return w.groups ? (int)((long long)g * w.total / w.groups) : g * (int)p.chunk_tiles;
+}
+
+// Block-wide (every thread calls it; the result is uniform).  The host keeps
+// T = hkv * gsplit * sum U_b below 2^31.
+__device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, SplitShared& sh) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nb = (int)p.batch;
+    int s = 0;
+    for (int b = threadIdx.x; b < nb; b += kWaves * 64) s += item_tiles(p, b);
+#pragma unroll
+    for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) sh.wsum[wave] = s;
+    __syncthreads();
+    int units = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) units += sh.wsum[w];
+    WorkSplit r;
+    r.total = __builtin_amdgcn_readfirstlane(units) * ips;
+    const int g = blockIdx.x;
+    if (p.chunk_tiles) {
+        r.groups = 0;
+        r.lo = (int)min((long long)g * p.chunk_tiles, (long long)r.total);
+        r.hi = (int)min((long long)r.lo + p.chunk_tiles, (long long)r.total);
+    } else {
+        r.groups = min((int)gridDim.x, r.total);
+        r.lo = g < r.groups ? split_lo(p, r, g) : r.total;
+        r.hi = g < r.groups ? split_lo(p, r, g + 1) : r.total;
+    }
+    r.b = 0;
+    r.seq0 = 0;
+    if (r.lo >= r.hi) return r;
+    // the sequence holding tile lo: exclusive prefix of U_b * ips, 256 sequences a pass
+    int carry = 0;
+    for (int base = 0; base < nb; base += kWaves * 64) {
+        const int b = base + (int)threadIdx.x;
+        const int u = b < nb ? item_tiles(p, b) : 0;
+        int x = u;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o);
+            if (lane >= o) x += y;
+        }
+        __syncthreads();  // earlier readers of wsum are done
+        if (lane == 63) sh.wsum[wave] = x;
+        __syncthreads();
+        int before = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            before += w < wave ? sh.wsum[w] : 0;
+            all += sh.wsum[w];
+        }
+        const int excl = (carry + before + x - u) * ips;
+        if (u > 0 && excl <= r.lo && r.lo < excl + u * ips) {
+            sh.b = b;
+            sh.seq0 = excl;
+        }
+        carry += all;
+    }
+    __syncthreads();
+    r.b = __builtin_amdgcn_readfirstlane(sh.b);
+    r.seq0 = __builtin_amdgcn_readfirstlane(sh.seq0);
+    return r;
+}
+
+// Partials cross workgroups that may sit on different XCDs, whose L2 caches are not
+// coherent with each other.  They are stored and loaded with device-scope accesses,
+// which write through to / read from the device's coherence point, so neither side
+// needs an agent-scope fence (a write-back or invalidation of the whole L2).
+__device__ __forceinline__ void store_device(float* ptr, float v) {
+    __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_device(const float* ptr) {
+    return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Position in the sequence-major order of work items (all fields wave-uniform).  Work
+// item y of sequence b covers kv head y / gsplit and query heads GW*y .. GW*y + GW - 1.
+struct ItemCursor {
+    int b;      // sequence
+    int seq0;   // first tile of the sequence
+    int U;      // tiles per work item of this sequence
+    int y;      // work item within the sequence
+    int item0;  // first tile of the work item
+};
+
+// the work item holding the workgroup's first tile
+__device__ __forceinline__ ItemCursor cursor_at(const DecodeParams& p, const WorkSplit& w) {
+    ItemCursor c;
+    c.b = w.b;
+    c.seq0 = w.seq0;
+    c.U = item_tiles(p, w.b);
+    c.y = (w.lo - w.seq0) / c.U;
+    c.item0 = c.seq0 + c.y * c.U;
+    return c;
+}
+
+// the next work item; callers only step onto items that hold a tile below T
+__device__ __forceinline__ void cursor_next(const DecodeParams& p, int ips, ItemCursor& c) {
+    if (c.y + 1 < ips) {
+        ++c.y;
+        c.item0 += c.U;
+    } else {
+        c.seq0 += c.U * ips;
+        ++c.b;
+        c.U = item_tiles(p, c.b);
+        c.y = 0;
+        c.item0 = c.seq0;
+    }
+}
+
+// One wave merges the kWaves states of one item segment held in LDS (st[w][h] =
+// {max, sum, acc[D]}, written by wave w) and writes the output rows of a whole work
+// item, or else the workgroup's partial `pslot` (0: its first segment, 1: its last).
+template <int D, int GW>
+__device__ __forceinline__ void merge_segment(const DecodeParams& p, const float (*st)[GW][D + 2], int lane,
+                                              size_t row0, bool whole, int pslot) {
+    float* pacc = p.part_acc + ((size_t)blockIdx.x * 2 + pslot) * GW * D;
+    float* pml = p.part_ml + ((size_t)blockIdx.x * 2 + pslot) * GW * 2;
+    for (int idx = lane; idx < GW * D; idx += 64) {
+        const int h = idx / D;
+        const int d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) M = fmaxf(M, st[v][h][0]);
+        float a = 0.f, l = 0.f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) {
+            const float f = exp2f(st[v][h][0] - M);
+            a = fmaf(st[v][h][2 + d], f, a);
+            l = fmaf(st[v][h][1], f, l);
+        }
+        if (whole) {
+            p.out[(row0 + h) * D + d] = l > 0.f ? a / l : 0.f;
+        } else {
+            store_device(pacc + idx, a);
+            if (d == 0) {
+                store_device(pml + 2 * h, M);
+                store_device(pml + 2 * h + 1, l);
+            }
+        }
+    }
+}
+
+// Block-wide, after every wave has merged its segments: count this workgroup's partials
+// (at most two: its first segment `first` and its last `last`) at their work items; the
+// workgroup that arrives last at an item merges all of the item's partials.
+template <int D, int GW>
+__device__ __forceinline__ void arrive_partials(const DecodeParams& p, const WorkSplit& w, SplitShared& sh, int ips,
+                                                const ItemCursor& first, const ItemCursor& last) {
+    const bool part0 = !(first.item0 >= w.lo && first.item0 + first.U <= w.hi);
+    const bool part1 = last.item0 != first.item0 && !(last.item0 >= w.lo && last.item0 + last.U <= w.hi);
+    if (!part0 && !part1) return;
+    int tid = (int)threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    // every wave's partial stores have completed (they write through to the device's
+    // coherence point, so no L2 write-back is needed) before the arrivals are counted
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int k = 0; k < 2; ++k) {
+        const ItemCursor& c = k == 0 ? first : last;
+        const bool has = k == 0 ? part0 : part1;
+        if (!has) continue;
+        // the workgroups whose ranges meet the item's tiles [item0, item0 + U)
+        const int g0 = w.groups ? (int)(((long long)(c.item0 + 1) * w.groups - 1) / w.total)
+                                : c.item0 / (int)p.chunk_tiles;
+        const int g1 = w.groups ? (int)(((long long)(c.item0 + c.U) * w.groups - 1) / w.total)
+                                : (c.item0 + c.U - 1) / (int)p.chunk_tiles;
+        if (tid == 0) {
+            const uint32_t item = (uint32_t)(c.b * ips + c.y);
+            const uint32_t seen = atomicAdd(p.arrivals + item, 1u);
+            const int last_in = seen == (uint32_t)(g1 - g0);
+            if (last_in) __hip_atomic_store(p.arrivals + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sh.last = last_in;
+        }
+        __syncthreads();
+        const int merge = sh.last;
+        __syncthreads();  // sh.last is rewritten for the second item
+        if (!merge) continue;
+        const int first_starts_inside = split_lo(p, w, g0) < c.item0 ? 1 : 0;
+        const size_t row0 = (size_t)c.b * p.hq + (size_t)c.y * GW;
+        for (int idx = tid; idx < GW * D; idx += kWaves * 64) {
+            const int h = idx / D;
+            const int d = idx % D;
+            float M = -INFINITY;
+            for (int g = g0; g <= g1; ++g) {
+                const size_t s = (size_t)g * 2 + (g == g0 ? first_starts_inside : 0);
+                M = fmaxf(M, load_device(p.part_ml + (s * GW + h) * 2));
+            }
+            float a = 0.f, l = 0.f;
+            for (int g = g0; g <= g1; ++g) {
+                const size_t s = (size_t)g * 2 + (g == g0 ? first_starts_inside : 0);
+                const float f = exp2f(load_device(p.part_ml + (s * GW + h) * 2) - M);
+                a = fmaf(load_device(p.part_acc + (s * GW + h) * D + d), f, a);
+                l = fmaf(load_device(p.part_ml + (s * GW + h) * 2 + 1), f, l);
+            }
+            p.out[(row0 + h) * D + d] = l > 0.f ? a / l : 0.f;
+        }
+    }
+}
+
+// Merge the kWaves per-wave states of one segment (tiles [tile_begin, tile_end) of the
+// work item `item`, whose U tiles start at global tile item0) and write the output row,
+// or the partial and, in the last workgroup to arrive, the merged output row.
+template <int D, int GW>
+__device__ __forceinline__ void finish_segment(const DecodeParams& p, const float (*comb)[GW][D + 2],
+                                               const WorkSplit& w, SplitShared& sh, int b, int hq0,
+                                               int item, int item0, int U, int tile_begin, int tile_end,
+                                               int slot) {
+    const bool whole = tile_begin == 0 && tile_end == U;
+    const size_t row0 = (size_t)b * p.hq + hq0;
+    // thread index behind an opaque copy: the address arithmetic below then stays here
+    // instead of being hoisted out of the caller's loops into registers that would
+    // stay live through the tile loop
+    int tid = (int)threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    float* pacc = p.part_acc + ((size_t)blockIdx.x * 2 + slot) * GW * D;
+    float* pml = p.part_ml + ((size_t)blockIdx.x * 2 + slot) * GW * 2;
+    for (int idx = tid; idx < GW * D; idx += kWaves * 64) {
+        const int h = idx / D;
+        const int d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) M = fmaxf(M, comb[v][h][0]);
+        float a = 0.f, l = 0.f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) {
+            const float f = exp2f(comb[v][h][0] - M);
+            a = fmaf(comb[v][h][2 + d], f, a);
+            l = fmaf(comb[v][h][1], f, l);
+        }
+        if (whole) {
+            p.out[(row0 + h) * D + d] = l > 0.f ? a / l : 0.f;
+        } else {
+            store_device(pacc + idx, a);
+            if (d == 0) {
+                store_device(pml + 2 * h, M);
+                store_device(pml + 2 * h + 1, l);
+            }
+        }
+    }
+    if (whole) return;
+    // the workgroups whose ranges meet [item0, item0 + U)
+    const int g0 = w.groups ? (int)(((long long)(item0 + 1) * w.groups - 1) / w.total)
+                            : item0 / (int)p.chunk_tiles;
+    const int g1 = w.groups ? (int)(((long long)(item0 + U) * w.groups - 1) / w.total)
+                            : (item0 + U - 1) / (int)p.chunk_tiles;
+    // this wave's partial stores have completed (they write through to the device's
+    // coherence point, so no L2 write-back is needed) before the arrival is counted
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t seen = atomicAdd(p.arrivals + item, 1u);
+        const int last = seen == (uint32_t)(g1 - g0);
+        if (last) __hip_atomic_store(p.arrivals + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh.last = last;
+    }
+    __syncthreads();
+    if (!sh.last) return;
+    const int first_starts_inside = split_lo(p, w, g0) < item0 ? 1 : 0;
+    for (int idx = tid; idx < GW * D; idx += kWaves * 64) {
+        const int h = idx / D;
+        const int d = idx % D;
+        float M = -INFINITY;
+        for (int g = g0; g <= g1; ++g) {
+            const size_t s = (size_t)g * 2 + (g == g0 ? first_starts_inside : 0);
+            M = fmaxf(M, load_device(p.part_ml + (s * GW + h) * 2));
+        }
+        float a = 0.f, l = 0.f;
+        for (int g = g0; g <= g1; ++g) {
+            const size_t s = (size_t)g * 2 + (g == g0 ? first_starts_inside : 0);
+            const float f = exp2f(load_device(p.part_ml + (s * GW + h) * 2) - M);
+            a = fmaf(load_device(p.part_acc + (s * GW + h) * D + d), f, a);
+            l = fmaf(load_device(p.part_ml + (s * GW + h) * 2 + 1), f, l);
+        }
+        p.out[(row0 + h) * D + d] = l > 0.f ? a / l : 0.f;
     }
 }
 

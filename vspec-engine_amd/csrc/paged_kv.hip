@@ -14,7 +14,10 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <mutex>
 
 #include "vspec_rocm_paged.h"
 
@@ -870,12 +873,87 @@ void* library_workspace(size_t bytes) {
     return w.ptr;
 }
 
+// Arrival counters of the MFMA decode split: one zeroed array per (device, stream),
+// grow-only.  Every launch returns the counters it used to zero, so a stream's array
+// stays valid for any later shape; launches on different streams never share one.
+struct Arrivals {
+    hipStream_t stream = nullptr;
+    uint32_t* ptr = nullptr;
+    size_t count = 0;
+    bool used = false;
+};
+constexpr int kArrivalStreams = 32;
+Arrivals g_arrivals[64][kArrivalStreams];
+std::mutex g_arrivals_mu;
+
+__global__ void fill_zero_u32(uint32_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+uint32_t* arrival_counters(size_t count, hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_err("paged_decode: no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_arrivals_mu);
+    Arrivals* slot = nullptr;
+    Arrivals* free_slot = nullptr;
+    for (Arrivals& a : g_arrivals[dev]) {
+        if (a.used && a.stream == stream) slot = &a;
+        else if (!a.used && !free_slot) free_slot = &a;
+    }
+    if (!slot) {
+        if (!free_slot) {
+            set_err("paged_decode: more than %d streams on one device", kArrivalStreams);
+            return nullptr;
+        }
+        slot = free_slot;
+        slot->used = true;
+        slot->stream = stream;
+    }
+    if (slot->count >= count) return slot->ptr;
+    if (slot->ptr) (void)hipFree(slot->ptr);  // waits for the device
+    slot->ptr = nullptr;
+    slot->count = 0;
+    const size_t n = count < 4096 ? 4096 : count;
+    if (hipMalloc(&slot->ptr, n * sizeof(uint32_t)) != hipSuccess) {
+        slot->ptr = nullptr;
+        set_err("paged_decode: cannot allocate %zu arrival counters", n);
+        return nullptr;
+    }
+    hipLaunchKernelGGL(fill_zero_u32, dim3((unsigned)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024)), dim3(256),
+                       0, stream, slot->ptr, n);
+    if (hipGetLastError() != hipSuccess) {
+        set_err("paged_decode: counter fill failed");
+        return nullptr;
+    }
+    slot->count = n;
+    return slot->ptr;
+}
+
+// workgroups per CU of the balanced MFMA split (VSPEC_ROCM_DECODE_WGS_PER_CU, 1..8)
+uint32_t decode_wgs_per_cu() {
+    static const uint32_t v = [] {
+        const char* e = getenv("VSPEC_ROCM_DECODE_WGS_PER_CU");
+        const long x = e ? strtol(e, nullptr, 10) : 0;
+        return x >= 1 && x <= 8 ? (uint32_t)x : 2u;
+    }();
+    return v;
+}
+
 struct DecodePlan {
     uint32_t gw;
     uint32_t gsplit;
     uint32_t tiles_per_part;
     uint32_t max_parts;
     size_t ws_bytes;
+    // MFMA kernels (f16 / int4 pools): tiles of all work items split over grid_x workgroups
+    bool split;
+    uint32_t grid_x;
+    uint32_t chunk_tiles;
+    uint32_t max_tiles;
 };
 
 int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
@@ -896,6 +974,34 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
         return 0;
     }
     const uint32_t max_tiles = (d->max_ctx_len + kTile - 1) / kTile;
+    pl->split = d->kv.dtype != VSPEC_KV_F32;
+    if (pl->split) {
+        // every workgroup streams an equal share of all work items' tiles
+        const uint64_t bound = (uint64_t)d->batch * hkv * pl->gsplit * (max_tiles ? max_tiles : 1);
+        if (bound > (uint64_t)INT32_MAX) {
+            set_err("paged_decode: batch * work items * tiles exceeds 2^31");
+            return 0;
+        }
+        uint64_t grid;
+        if (d->partition_tokens) {
+            if (d->partition_tokens % kTile) {
+                set_err("paged_decode: partition_tokens must be a multiple of %d", kTile);
+                return 0;
+            }
+            pl->chunk_tiles = d->partition_tokens / kTile;
+            grid = (bound + pl->chunk_tiles - 1) / pl->chunk_tiles;
+        } else {
+            pl->chunk_tiles = 0;
+            grid = (uint64_t)decode_wgs_per_cu() * (uint64_t)num_cus();
+            if (grid > bound) grid = bound;
+        }
+        pl->grid_x = (uint32_t)(grid ? grid : 1);
+        pl->max_tiles = max_tiles;
+        pl->tiles_per_part = 0;
+        pl->max_parts = 1;
+        pl->ws_bytes = (size_t)pl->grid_x * 2 * pl->gw * (2 + d->kv.head_dim) * sizeof(float);
+        return 1;
+    }
     uint32_t tpp;
     if (d->partition_tokens) {
         if (d->partition_tokens % kTile) {
@@ -1349,9 +1455,19 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
     p.alpha = desc->clamp_alpha > 0.f ? desc->clamp_alpha : 4.5f;
     p.logit_clip = three ? 24.0f * kLog2e : INFINITY;
     p.input_clip = three ? 16.0f : INFINITY;
+    p.arrivals = nullptr;
+    p.batch = desc->batch;
+    p.max_tiles = pl.max_tiles;
+    p.chunk_tiles = pl.chunk_tiles;
 
     hipStream_t s = (hipStream_t)desc->stream;
-    const dim3 grid(pl.max_parts, desc->kv.num_kv_heads * pl.gsplit, desc->batch);
+    if (pl.split) {
+        // partial slots [grid][2][GW] of (max, sum) then of acc[D]
+        p.part_acc = (float*)ws + (size_t)pl.grid_x * 2 * pl.gw * 2;
+        p.arrivals = arrival_counters((size_t)desc->batch * desc->kv.num_kv_heads * pl.gsplit, s);
+        if (!p.arrivals) return 0;
+    }
+    const dim3 grid = pl.split ? dim3(pl.grid_x) : dim3(pl.max_parts, desc->kv.num_kv_heads * pl.gsplit, desc->batch);
     int ok = 0;
     switch (desc->kv.dtype) {
         case VSPEC_KV_F32: ok = dispatch_d<VSPEC_KV_F32>(D, pl.gw, p, grid, s); break;
@@ -1362,8 +1478,8 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
         set_err("paged_decode: no kernel for head_dim %u, group %u", D, pl.gw);
         return 0;
     }
-    HIP_CHECK(hipGetLastError(), "decode_partial launch");
-    if (pl.max_parts > 1) {
+    HIP_CHECK(hipGetLastError(), "decode launch");
+    if (!pl.split && pl.max_parts > 1) {
         const dim3 cg(desc->num_q_heads, desc->batch);
         if (D == 64) hipLaunchKernelGGL(decode_combine<64>, cg, dim3(64), 0, s, p);
         else hipLaunchKernelGGL(decode_combine<128>, cg, dim3(128), 0, s, p);
