@@ -272,7 +272,7 @@ struct SplitShared {
     int wsum[kWaves];
     int b;
     int seq0;
-    int last;
+    int last[2];
 };
 
 __device__ __forceinline__ int item_tiles(const DecodeParams& p, int b) {
@@ -427,6 +427,69 @@ __device__ __forceinline__ void merge_segment(const DecodeParams& p, const float
     }
 }
 
+// Block-wide, last arrival at work item c: merge the partials of the workgroups g0..g1
+// whose ranges meet its tiles, NBATCH workgroups per batch with all of a batch's loads
+// in flight together (a chain of one load at a time would cost a memory latency each).
+template <int D, int GW>
+__device__ __forceinline__ void merge_group(const DecodeParams& p, const WorkSplit& w, const ItemCursor& c,
+                                            int tid) {
+    constexpr int NT = kWaves * 64;
+    constexpr int K = (GW * D + NT - 1) / NT;  // outputs per thread: idx = tid + NT * k
+    constexpr int NBATCH = 8;
+    const int g0 = w.groups ? (int)(((long long)(c.item0 + 1) * w.groups - 1) / w.total)
+                            : c.item0 / (int)p.chunk_tiles;
+    const int g1 = w.groups ? (int)(((long long)(c.item0 + c.U) * w.groups - 1) / w.total)
+                            : (c.item0 + c.U - 1) / (int)p.chunk_tiles;
+    const int first_inside = split_lo(p, w, g0) < c.item0 ? 1 : 0;
+    // running merge per output in log2 units; -1e30 (not -inf) keeps exp2 finite
+    float M[K], A[K], Ls[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        M[k] = -1e30f;
+        A[k] = 0.f;
+        Ls[k] = 0.f;
+    }
+    for (int g = g0; g <= g1; g += NBATCH) {
+        float mb[NBATCH][K], lb[NBATCH][K], ab[NBATCH][K];
+#pragma unroll
+        for (int i = 0; i < NBATCH; ++i) {
+            const bool valid = g + i <= g1;
+            const int gg = valid ? g + i : g1;
+            const size_t slot = (size_t)gg * 2 + (gg == g0 ? first_inside : 0);
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const int idx = min(tid + NT * k, GW * D - 1);
+                const int h = idx / D;
+                const int d = idx % D;
+                const float m = load_device(p.part_ml + (slot * GW + h) * 2);
+                const float l = load_device(p.part_ml + (slot * GW + h) * 2 + 1);
+                const float a = load_device(p.part_acc + (slot * GW + h) * D + d);
+                mb[i][k] = valid ? m : -1e30f;
+                lb[i][k] = valid ? l : 0.f;
+                ab[i][k] = valid ? a : 0.f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NBATCH; ++i) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const float nm = fmaxf(M[k], mb[i][k]);
+                const float fo = exp2f(M[k] - nm);
+                const float fn = exp2f(mb[i][k] - nm);
+                A[k] = fmaf(ab[i][k], fn, A[k] * fo);
+                Ls[k] = fmaf(lb[i][k], fn, Ls[k] * fo);
+                M[k] = nm;
+            }
+        }
+    }
+    const size_t row0 = (size_t)c.b * p.hq + (size_t)c.y * GW;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int idx = tid + NT * k;
+        if (idx < GW * D) p.out[(row0 + idx / D) * D + idx % D] = Ls[k] > 0.f ? A[k] / Ls[k] : 0.f;
+    }
+}
+
 // Block-wide, after every wave has merged its segments: count this workgroup's partials
 // (at most two: its first segment `first` and its last `last`) at their work items; the
 // workgroup that arrives last at an item merges all of the item's partials.
@@ -442,46 +505,32 @@ __device__ __forceinline__ void arrive_partials(const DecodeParams& p, const Wor
     // coherence point, so no L2 write-back is needed) before the arrivals are counted
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int k = 0; k < 2; ++k) {
-        const ItemCursor& c = k == 0 ? first : last;
-        const bool has = k == 0 ? part0 : part1;
-        if (!has) continue;
-        // the workgroups whose ranges meet the item's tiles [item0, item0 + U)
-        const int g0 = w.groups ? (int)(((long long)(c.item0 + 1) * w.groups - 1) / w.total)
-                                : c.item0 / (int)p.chunk_tiles;
-        const int g1 = w.groups ? (int)(((long long)(c.item0 + c.U) * w.groups - 1) / w.total)
-                                : (c.item0 + c.U - 1) / (int)p.chunk_tiles;
-        if (tid == 0) {
-            const uint32_t item = (uint32_t)(c.b * ips + c.y);
+    // both arrivals at once: thread k counts item k (first, last)
+    if (tid < 2) {
+        const bool has = tid == 0 ? part0 : part1;
+        const int b = tid == 0 ? first.b : last.b;
+        const int y = tid == 0 ? first.y : last.y;
+        const int U = tid == 0 ? first.U : last.U;
+        const int item0 = tid == 0 ? first.item0 : last.item0;
+        int last_in = 0;
+        if (has) {
+            // the workgroups whose ranges meet the item's tiles [item0, item0 + U)
+            const int g0 = w.groups ? (int)(((long long)(item0 + 1) * w.groups - 1) / w.total)
+                                    : item0 / (int)p.chunk_tiles;
+            const int g1 = w.groups ? (int)(((long long)(item0 + U) * w.groups - 1) / w.total)
+                                    : (item0 + U - 1) / (int)p.chunk_tiles;
+            const uint32_t item = (uint32_t)(b * ips + y);
             const uint32_t seen = atomicAdd(p.arrivals + item, 1u);
-            const int last_in = seen == (uint32_t)(g1 - g0);
+            last_in = seen == (uint32_t)(g1 - g0);
             if (last_in) __hip_atomic_store(p.arrivals + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            sh.last = last_in;
         }
-        __syncthreads();
-        const int merge = sh.last;
-        __syncthreads();  // sh.last is rewritten for the second item
-        if (!merge) continue;
-        const int first_starts_inside = split_lo(p, w, g0) < c.item0 ? 1 : 0;
-        const size_t row0 = (size_t)c.b * p.hq + (size_t)c.y * GW;
-        for (int idx = tid; idx < GW * D; idx += kWaves * 64) {
-            const int h = idx / D;
-            const int d = idx % D;
-            float M = -INFINITY;
-            for (int g = g0; g <= g1; ++g) {
-                const size_t s = (size_t)g * 2 + (g == g0 ? first_starts_inside : 0);
-                M = fmaxf(M, load_device(p.part_ml + (s * GW + h) * 2));
-            }
-            float a = 0.f, l = 0.f;
-            for (int g = g0; g <= g1; ++g) {
-                const size_t s = (size_t)g * 2 + (g == g0 ? first_starts_inside : 0);
-                const float f = exp2f(load_device(p.part_ml + (s * GW + h) * 2) - M);
-                a = fmaf(load_device(p.part_acc + (s * GW + h) * D + d), f, a);
-                l = fmaf(load_device(p.part_ml + (s * GW + h) * 2 + 1), f, l);
-            }
-            p.out[(row0 + h) * D + d] = l > 0.f ? a / l : 0.f;
-        }
+        sh.last[tid] = last_in;
     }
+    __syncthreads();
+    const int merge0 = sh.last[0];
+    const int merge1 = sh.last[1];
+    if (merge0) merge_group<D, GW>(p, w, first, tid);
+    if (merge1) merge_group<D, GW>(p, w, last, tid);
 }
 
 // Merge the kWaves per-wave states of one segment (tiles [tile_begin, tile_end) of the
@@ -538,28 +587,17 @@ __device__ __forceinline__ void finish_segment(const DecodeParams& p, const floa
         const uint32_t seen = atomicAdd(p.arrivals + item, 1u);
         const int last = seen == (uint32_t)(g1 - g0);
         if (last) __hip_atomic_store(p.arrivals + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sh.last = last;
+        sh.last[0] = last;
     }
     __syncthreads();
-    if (!sh.last) return;
-    const int first_starts_inside = split_lo(p, w, g0) < item0 ? 1 : 0;
-    for (int idx = tid; idx < GW * D; idx += kWaves * 64) {
-        const int h = idx / D;
-        const int d = idx % D;
-        float M = -INFINITY;
-        for (int g = g0; g <= g1; ++g) {
-            const size_t s = (size_t)g * 2 + (g == g0 ? first_starts_inside : 0);
-            M = fmaxf(M, load_device(p.part_ml + (s * GW + h) * 2));
-        }
-        float a = 0.f, l = 0.f;
-        for (int g = g0; g <= g1; ++g) {
-            const size_t s = (size_t)g * 2 + (g == g0 ? first_starts_inside : 0);
-            const float f = exp2f(load_device(p.part_ml + (s * GW + h) * 2) - M);
-            a = fmaf(load_device(p.part_acc + (s * GW + h) * D + d), f, a);
-            l = fmaf(load_device(p.part_ml + (s * GW + h) * 2 + 1), f, l);
-        }
-        p.out[(row0 + h) * D + d] = l > 0.f ? a / l : 0.f;
-    }
+    if (!sh.last[0]) return;
+    ItemCursor c;
+    c.b = b;
+    c.y = (int)(hq0 / GW);
+    c.U = U;
+    c.item0 = item0;
+    c.seq0 = 0;
+    merge_group<D, GW>(p, w, c, tid);
 }
 
 }  // namespace vkv
