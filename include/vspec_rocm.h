@@ -117,14 +117,14 @@ typedef struct VspecPagedAttnDesc {
     const int32_t* block_tables;     /* device [batch][max_blocks_per_seq] */
     uint32_t max_blocks_per_seq;
     const int32_t* ctx_lens;         /* device [batch] */
-    uint32_t max_ctx_len;            /* host upper bound of ctx_lens (grid sizing) */
+    uint32_t max_ctx_len;            /* host upper bound of ctx_lens (sizes the workspace) */
     const float* q;                  /* device [batch][Hq][D] f32 */
     float* out;                      /* device [batch][Hq][D] f32 (ctx 0 -> zeros) */
     float scale;                     /* <= 0: 1/sqrtf(D) */
     int32_t numerics;                /* VSPEC_NUMERICS_PLAIN or VSPEC_NUMERICS_3BIT */
     float clamp_alpha;               /* <= 0: 4.5 */
-    uint32_t partition_tokens;       /* split-K partition length, multiple of 16; 0: auto */
-    void* workspace;                 /* device scratch or NULL (library-managed) */
+    uint32_t partition_tokens;       /* tokens per workgroup range (multiple of 16); 0: even split */
+    void* workspace;                 /* device scratch (no init needed) or NULL: library's */
     size_t workspace_bytes;
     void* stream;                    /* hipStream_t or NULL */
 } VspecPagedAttnDesc;

@@ -304,6 +304,66 @@ def test_decode_partition_invariance(oracle, gpu):
     check_attention(oracle, case, outs[0], 0)
 
 
+def test_decode_back_to_back_and_streams(oracle, gpu):
+    """Split work items are merged in-kernel through per-(device, stream) arrival
+    counters that every launch returns to zero: decodes of different shapes and dtypes
+    back to back on one stream, then on two streams at once with their own workspaces,
+    must all reproduce the first run bit for bit (every output row written: the output
+    is NaN-filled before each launch)."""
+    import torch
+    import vspec_rocm as vr
+
+    say("[back-to-back] build")
+    cases = [make_case(oracle, DTYPE_F16, 5, 32, 8, 128, 16, [700, 2049, 33, 1500, 911], seed=51),
+             make_case(oracle, DTYPE_INT4, 3, 16, 4, 128, 16, [1777, 64, 1201], seed=52),
+             make_case(oracle, DTYPE_F16, 9, 8, 2, 64, 32, [300, 1, 77, 1023, 640, 0, 5, 260, 999], seed=53)]
+    pools = [build_both(oracle, c, gpu) for c in cases]
+    dev_args = [(torch.from_numpy(c.tables).to(gpu), torch.from_numpy(c.ctx).to(gpu), torch.from_numpy(c.q).to(gpu))
+                for c in cases]
+
+    def decode(i, pt=0, stream=None, workspace=None):
+        c = cases[i]
+        bt, cl, q = dev_args[i]
+        out = torch.full_like(q, float("nan"))
+        vr.paged_decode(pools[i], bt, cl, q, max_ctx_len=c.tmax, numerics=1, partition_tokens=pt, out=out,
+                        stream=stream, workspace=workspace)
+        return out
+
+    first = [decode(i).cpu().numpy() for i in range(len(cases))]
+    for i, c in enumerate(cases):
+        check_attention(oracle, c, first[i], 1)
+    say("[back-to-back] alternating shapes")
+    for rep in range(4):
+        for i in (2, 0, 1, 0, 2, 1):
+            got = decode(i).cpu().numpy()
+            assert np.array_equal(got, first[i]), f"rep {rep} case {i}: differs from the first run"
+    say("[back-to-back] chunked split between balanced launches")
+    for i in range(len(cases)):
+        # another split moves the lazy running max; int4 rounds p * scale to fp16 once
+        # per token (relative 2^-12), so its results move by up to 2.4e-4 * max|v|
+        v = cases[i].v_tokens
+        vmax = float(np.abs(v.view(np.float16) if v.dtype == np.uint16 else v).astype(np.float32).max())
+        tol = 1e-5 if cases[i].dtype == DTYPE_F16 else 2.4e-4 * vmax + 1e-5
+        assert np.abs(decode(i, pt=32).cpu().numpy() - first[i]).max() < tol
+        assert np.array_equal(decode(i).cpu().numpy(), first[i])
+    say("[back-to-back] two streams")
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i in range(len(cases)):
+            bt, cl, q = dev_args[i]
+            d = vr.make_decode_desc(pools[i], bt, cl, q, q, cases[i].tmax, 1)
+            nbytes = max(vr.decode_workspace_bytes(d), 4)
+            for s in (s1, s2):
+                ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+                with torch.cuda.stream(s):
+                    outs.append((i, decode(i, stream=s.cuda_stream, workspace=ws), ws))
+    torch.cuda.synchronize()
+    for i, o, _ in outs:
+        assert np.array_equal(o.cpu().numpy(), first[i])
+
+
 # ----------------------------------------------------------------------------- config 5
 @pytest.mark.parametrize("mode", [0, 1])
 def test_config5_chunk_evict_compact(oracle, gpu, mode):

@@ -74,22 +74,6 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     if (ws.lo >= ws.hi) return;
     const ItemCursor first = cursor_at(p, ws);
 
-    // q rows of the first kQStage segments (rows GW*y .. GW*y + GW - 1 of sequence b are
-    // contiguous); merge slot s serves segment s first
-    {
-        ItemCursor c = first;
-        for (int s = 0; s < kQStage; ++s) {
-            const float* qrow = p.q + ((size_t)c.b * p.hq + (size_t)c.y * GW) * D;
-            for (int i = threadIdx.x; i < GW * D; i += kWaves * 64) qraw[s][i / D][i % D] = qrow[i];
-            if (c.item0 + c.U >= ws.hi) break;
-            cursor_next(p, ips, c);
-        }
-        if (threadIdx.x < kSlots) {
-            slot_cnt[threadIdx.x] = 0;
-            slot_seg[threadIdx.x] = threadIdx.x;
-        }
-    }
-    __syncthreads();
 
     // ---- q' = clip(q) * scale * log2(e) of work item c (segment s) for this wave, and
     // the B operands of the QK MFMAs: column n < GW holds head n, split hi + lo ----
@@ -394,15 +378,33 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     ItemCursor pc = first;  // work item of the tiles being processed
     int seg = 0;            // its segment index in this workgroup
     int pctx = min(max(as_const(p.ctx_lens)[pc.b], 0), ctx_cap);
-    reset();
-    qprep(0, pc);
     const int len = ws.hi - ws.lo;
     const int t0 = ws.lo + wave;
     const int nt = wave < len ? (len - wave + kWaves - 1) / kWaves : 0;
     Frags<D> f[NB];
     bool ok[NB];
+    // the first tiles' loads go out before the q rows are staged, so that the two
+    // latencies overlap (the barrier below does not wait for them)
 #pragma unroll
     for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * kWaves, f[u]);
+    // q rows of the first kQStage segments (rows GW*y .. GW*y + GW - 1 of sequence b are
+    // contiguous); merge slot s serves segment s first
+    {
+        ItemCursor c = first;
+        for (int s = 0; s < kQStage; ++s) {
+            const float* qrow = p.q + ((size_t)c.b * p.hq + (size_t)c.y * GW) * D;
+            for (int i = threadIdx.x; i < GW * D; i += kWaves * 64) qraw[s][i / D][i % D] = qrow[i];
+            if (c.item0 + c.U >= ws.hi) break;
+            cursor_next(p, ips, c);
+        }
+        if (threadIdx.x < kSlots) {
+            slot_cnt[threadIdx.x] = 0;
+            slot_seg[threadIdx.x] = threadIdx.x;
+        }
+    }
+    __syncthreads();
+    reset();
+    qprep(0, pc);
     for (int k = 0; k < nt; k += NB) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {

@@ -285,23 +285,8 @@ __device__ __forceinline__ int split_lo(const DecodeParams& p, const WorkSplit& 
     return w.groups ? (int)((long long)g * w.total / w.groups) : g * (int)p.chunk_tiles;
 }
 
-// Block-wide (every thread calls it; the result is uniform).  The host keeps
-// T = hkv * gsplit * sum U_b below 2^31.
-__device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, SplitShared& sh) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int nb = (int)p.batch;
-    int s = 0;
-    for (int b = threadIdx.x; b < nb; b += kWaves * 64) s += item_tiles(p, b);
-#pragma unroll
-    for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
-    if (lane == 0) sh.wsum[wave] = s;
-    __syncthreads();
-    int units = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) units += sh.wsum[w];
-    WorkSplit r;
-    r.total = __builtin_amdgcn_readfirstlane(units) * ips;
+// this workgroup's tiles [lo, hi) once T is known
+__device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r) {
     const int g = blockIdx.x;
     if (p.chunk_tiles) {
         r.groups = 0;
@@ -312,6 +297,59 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         r.lo = g < r.groups ? split_lo(p, r, g) : r.total;
         r.hi = g < r.groups ? split_lo(p, r, g + 1) : r.total;
     }
+}
+
+// Block-wide (every thread calls it; the result is uniform).  The host keeps
+// T = hkv * gsplit * sum U_b below 2^31.
+__device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, SplitShared& sh) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nb = (int)p.batch;
+    WorkSplit r;
+    if (nb <= kWaves * 64) {
+        // one sequence per thread: the total and the search come from one scan
+        const int b = (int)threadIdx.x;
+        const int u = b < nb ? item_tiles(p, b) : 0;
+        int x = u;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o);
+            if (lane >= o) x += y;
+        }
+        if (lane == 63) sh.wsum[wave] = x;
+        __syncthreads();
+        int before = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            before += w < wave ? sh.wsum[w] : 0;
+            all += sh.wsum[w];
+        }
+        r.total = __builtin_amdgcn_readfirstlane(all) * ips;
+        split_range(p, r);
+        r.b = 0;
+        r.seq0 = 0;
+        if (r.lo >= r.hi) return r;
+        const int excl = (before + x - u) * ips;
+        if (u > 0 && excl <= r.lo && r.lo < excl + u * ips) {
+            sh.b = b;
+            sh.seq0 = excl;
+        }
+        __syncthreads();
+        r.b = __builtin_amdgcn_readfirstlane(sh.b);
+        r.seq0 = __builtin_amdgcn_readfirstlane(sh.seq0);
+        return r;
+    }
+    int s = 0;
+    for (int b = threadIdx.x; b < nb; b += kWaves * 64) s += item_tiles(p, b);
+#pragma unroll
+    for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) sh.wsum[wave] = s;
+    __syncthreads();
+    int units = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) units += sh.wsum[w];
+    r.total = __builtin_amdgcn_readfirstlane(units) * ips;
+    split_range(p, r);
     r.b = 0;
     r.seq0 = 0;
     if (r.lo >= r.hi) return r;
