@@ -11,7 +11,7 @@ import sys
 import numpy as np
 import pytest
 
-from oracle.oracle import DTYPE_F16, DTYPE_F32, DTYPE_INT4, HostPool
+from oracle.oracle import DTYPE_F16, DTYPE_F32, DTYPE_INT4, HostPool, _f32p, _u8p, ptr
 from cases import GARBAGE, continuous_c4, make_case, qwen_c2
 
 pytestmark = pytest.mark.gpu
@@ -479,13 +479,22 @@ def _legacy_launch(q, k, v, mode):
     import vspec_rocm as vr
 
     T, H, D = k.shape
-    q = np.ascontiguousarray(q, np.float32)
     k = np.ascontiguousarray(k, np.float32)
     v = np.ascontiguousarray(v, np.float32)
-    out = np.full((H, D), 7.0, np.float32)
     cache = vr.VspecKVCache()
     cache.key, cache.value = k.ctypes.data, v.ctypes.data
     cache.max_tokens, cache.num_heads, cache.head_dim, cache.current_tokens = T, H, D, T
+    return _launch_cache(q, cache, mode)
+
+
+def _launch_cache(q, cache, mode):
+    """launch_attention over a prepared VspecKVCache (host buffers kept alive by the caller)."""
+    import ctypes as C
+    import os
+    import vspec_rocm as vr
+
+    q = np.ascontiguousarray(q, np.float32)
+    out = np.full((cache.num_heads, cache.head_dim), 7.0, np.float32)
     ctx = vr.VspecKernelContext()
     ctx.input, ctx.weight, ctx.output = q.ctypes.data, C.cast(C.pointer(cache), C.c_void_p), out.ctypes.data
     if mode:
@@ -529,6 +538,83 @@ def test_backend_legacy_context_matches_oracle(oracle, gpu, D, mode):
     out, err = _legacy_launch(q, k, v, mode)
     want = oracle.attention_ref(mode, q, k, v)
     assert np.abs(out - want).max() <= 1e-4, (np.abs(out - want).max(), err)
+
+
+def _int3_cache(oracle, k, v, block_size, mirror):
+    """A VspecKVCache with the reference's int3 codec on (kv_cache.c:160-215): codes and
+    scales made by the oracle's codec, and the fp32 mirror of the decoded rows on the
+    sides named in `mirror` ("k", "v"), NULL on the others.  Returns (cache, buffers,
+    decoded k, decoded v)."""
+    import vspec_rocm as vr
+
+    T, H, D = k.shape
+    pb, nb = (3 * D + 7) // 8, (D + block_size - 1) // block_size
+    bufs, dec = [], []
+    for x in (k, v):
+        codes = np.zeros((T * H, pb), np.uint8)
+        scales = np.zeros((T * H, nb), np.float32)
+        rows = np.zeros((T * H, D), np.float32)
+        for i, row in enumerate(np.asarray(x, np.float32).reshape(T * H, D)):
+            codes[i], scales[i] = oracle.int3_quantize_head(row, block_size)
+            oracle.lib.vo_int3_dequantize_head(ptr(codes[i], _u8p), ptr(scales[i], _f32p), D, block_size,
+                                               ptr(rows[i], _f32p))
+        bufs += [codes, scales, rows]
+        dec.append(rows.reshape(T, H, D))
+    cache = vr.VspecKVCache()
+    cache.max_tokens, cache.num_heads, cache.head_dim, cache.current_tokens = T, H, D, T
+    cache.int3_compressed = 1
+    cache.key_int3, cache.key_scales = bufs[0].ctypes.data, bufs[1].ctypes.data
+    cache.value_int3, cache.value_scales = bufs[3].ctypes.data, bufs[4].ctypes.data
+    cache.block_size, cache.blocks_per_head, cache.packed_head_bytes = block_size, nb, pb
+    cache.key = bufs[2].ctypes.data if "k" in mirror else None
+    cache.value = bufs[5].ctypes.data if "v" in mirror else None
+    return cache, bufs, dec[0], dec[1]
+
+
+@pytest.mark.parametrize("D,block_size", [(4, 32), (20, 16), (64, 16), (128, 32)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_backend_int3_cache_without_mirror(oracle, gpu, D, block_size, mode):
+    """An int3-compressed VspecKVCache with no fp32 mirror, which the reference's
+    accessors decode per read (kv_cache.c:296-362): the device decode gives the mirror's
+    rows bit for bit, so the result equals the run over the mirror exactly, on either side
+    alone and on both; and it matches the oracle's attention_ref over the decoded rows
+    within 1e-4.  D=20 has a partial scale block and codes that straddle bytes."""
+    H, T = 3, 70
+    q = oracle.normal(500 + D, H * D).reshape(H, D) * 2
+    k = oracle.normal(501 + D, T * H * D).reshape(T, H, D)
+    v = oracle.normal(502 + D, T * H * D).reshape(T, H, D)
+    k[::7, 2, 1] = 25.0
+    k[3, 0, :] = 0.0  # an all-zero head: scale 1.0
+    ref_out = None
+    for mirror in ("kv", "", "k", "v"):
+        cache, bufs, kd, vd = _int3_cache(oracle, k, v, block_size, mirror)
+        out, err = _launch_cache(q, cache, mode)
+        assert not np.all(out == 7.0), err
+        if ref_out is None:
+            ref_out = out
+            want = oracle.attention_ref(mode, q, kd, vd)
+            assert np.abs(out - want).max() <= 1e-4, np.abs(out - want).max()
+        else:
+            assert np.array_equal(out.view(np.uint32), ref_out.view(np.uint32)), mirror
+
+
+def test_backend_int3_cache_rejects_bad_geometry(oracle, gpu):
+    """A codec-only cache whose block_size is 0 or whose code rows are too short for
+    head_dim is refused with an error; the output is left as it was."""
+    import vspec_rocm as vr
+
+    H, T, D = 2, 5, 64
+    k = oracle.normal(7, T * H * D).reshape(T, H, D)
+    for field, bad in (("block_size", 0), ("packed_head_bytes", 23), ("blocks_per_head", 1)):
+        cache, bufs, _, _ = _int3_cache(oracle, k, k, 32, "")
+        setattr(cache, field, bad)
+        out, err = _launch_cache(np.ones((H, D), np.float32), cache, 0)
+        assert np.all(out == 7.0), field
+        assert "int3" in err, (field, err)
+    cache, bufs, _, _ = _int3_cache(oracle, k, k, 32, "")
+    cache.int3_compressed = 0
+    out, err = _launch_cache(np.ones((H, D), np.float32), cache, 0)
+    assert np.all(out == 7.0) and "neither" in err, err
 
 
 def test_backend_paged_flag(oracle, gpu):

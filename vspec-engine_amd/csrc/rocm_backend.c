@@ -12,9 +12,8 @@
 #include "vspec_rocm.h"
 
 void vspec_rocm_set_error_(const char* msg);
-int vspec_rocm_attention_contiguous_host(const float* q, const float* key, const float* value,
-                                         size_t tokens, size_t heads, size_t head_dim,
-                                         int32_t numerics, float* out);
+int vspec_rocm_attention_cache_host(const float* q, const VspecKVCache* cache, int32_t numerics,
+                                    float* out);
 
 /* The reference decides its attention numerics from the environment on every
  * call (three_bit_runtime_modules.c:18-24, :60-66); the contiguous path honours
@@ -53,14 +52,9 @@ static void rocm_launch_attention(VspecKernelContext* ctx) {
     if (cache->current_tokens == 0) {
         return; /* attention_ref.c:12-14 leaves the output untouched */
     }
-    if (!cache->key || !cache->value) {
-        vspec_rocm_set_error_("launch_attention: cache has no fp32 key/value rows");
-        return;
-    }
-    (void)vspec_rocm_attention_contiguous_host((const float*)ctx->input, cache->key, cache->value,
-                                               cache->current_tokens, cache->num_heads,
-                                               cache->head_dim, rocm_numerics_from_env(),
-                                               (float*)ctx->output);
+    /* fp32 rows, or int3 codes and scales when a compressed cache has no fp32 mirror */
+    (void)vspec_rocm_attention_cache_host((const float*)ctx->input, cache, rocm_numerics_from_env(),
+                                          (float*)ctx->output);
 }
 
 int vspec_rocm_backend_available(void) { return vspec_rocm_device_count() > 0 ? 1 : 0; }
