@@ -3,13 +3,16 @@
 
 A step is one layer's decode step for the whole batch: append one new K/V token
 per sequence into the paged fp16 cache (block-table append), then single-query
-GQA attention over the paged context.  Inputs are synthetic (seeded N(0,1)) and
-resident in HBM before timing starts.
+GQA attention over the paged context.  By default both run in one launch
+(vspec_rocm_paged_decode_step); --separate-append times the two-launch flow
+(vspec_rocm_kv_append, then vspec_rocm_paged_decode_attention).  Inputs are
+synthetic (seeded N(0,1)) and resident in HBM before timing starts.
 
 Printed JSON (one line on stdout):
   value      whole-step tokens/s = batch * steps / wall seconds
-  roofline   the attention kernels: algorithmic bytes per launch / the average
-             launch time from HIP events on the launch stream, against 8 TB/s
+  roofline   the decode kernel: algorithmic bytes per launch (with the fused
+             append's bytes) / the average launch time from HIP events on the
+             launch stream, against 8 TB/s
   cpu_baseline  the reference's own C path (oracle/_ref: append + capi gather +
              attention_ref) timed on a bounded sample of the same workload
 """
@@ -42,6 +45,12 @@ WORKLOADS = {
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def step_append_bytes(B, Hkv, D, dtype):
+    """The decode step's append: fp16 K and V rows read, pool rows (and int4 scales) written."""
+    row = {"f16": 2 * D, "f32": 4 * D, "int4": D // 2 + 2 * (D // 32)}[dtype]
+    return B * Hkv * 2 * (2 * D + row)
 
 
 def algorithmic_bytes(ctx_lens, Hq, Hkv, D, P, dtype):
@@ -103,7 +112,22 @@ def cpu_baseline(args, wl, pool, tables, ctx, q_all, out_gpu, mode):
                "sample": f"{S} of {wl['B']} sequences x ctx {T}: oracle restatement (gather + attention), 1 thread"}
     err = float(np.abs(out - out_gpu[:S].cpu().numpy()).max())
     res["parity_max_abs_vs_gpu"] = err
+    res.update(host_cpu())
     return res
+
+
+def host_cpu():
+    """The host the CPU baseline ran on: model name (as lscpu prints it) and usable threads."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": len(os.sched_getaffinity(0))}
 
 
 def cpu_baseline_ragged(wl, pool, tables, ctx, q_all, out_gpu, mode, S, lens):
@@ -128,7 +152,7 @@ def cpu_baseline_ragged(wl, pool, tables, ctx, q_all, out_gpu, mode, S, lens):
     return {"value": S / sec, "unit": "tokens/s", "cores": 1, "kind": "reference",
             "sample": f"{S} of {wl['B']} sequences (contexts {min(lens)}..{max(lens)}): reference decode "
                       f"step (paged append + capi.c gather + attention_ref, numerics {'R' if mode else 'P'}), 1 thread",
-            "parity_max_abs_vs_gpu": err}
+            "parity_max_abs_vs_gpu": err, **host_cpu()}
 
 
 def load_traffic(workload):
@@ -280,6 +304,8 @@ def main():
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--cpu-seqs", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--separate-append", action="store_true",
+                    help="append with its own launch before the decode launch (timed: the decode)")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="copy a buffer of this many MiB on the device once before warm-up, so that "
@@ -369,11 +395,16 @@ def main():
 
     def step(i):
         c = i % copies
-        vr.kv_append(pools[c], tables_l[c], pos, k_new, v_new)
+        if args.separate_append:
+            vr.kv_append(pools[c], tables_l[c], pos, k_new, v_new)
         ev = evs[i] if i >= 0 else None
         if ev:
             ev[0].record()
-        if not L.vspec_rocm_paged_decode_attention(C.byref(descs[c])):
+        if args.separate_append:
+            ok = L.vspec_rocm_paged_decode_attention(C.byref(descs[c]))
+        else:
+            ok = L.vspec_rocm_paged_decode_step(C.byref(descs[c]), k_new.data_ptr(), v_new.data_ptr(), vr.KV_F16)
+        if not ok:
             raise vr.VspecRocmError(vr.last_error())
         if ev:
             ev[1].record()
@@ -395,6 +426,8 @@ def main():
     med_attn_ms = attn_ms[len(attn_ms) // 2]
 
     alg = algorithmic_bytes(lens, Hq, Hkv, D, P, wl["dtype"])
+    if not args.separate_append:
+        alg += step_append_bytes(B, Hkv, D, wl["dtype"])
     achieved = alg / avg_attn_s / 1e9
     traffic = load_traffic(args.workload)
 
@@ -414,8 +447,9 @@ def main():
         "config": {"workload": args.workload, "batch": B, "ctx": T if min(lens) == T else [min(lens), T],
                    "q_heads": Hq, "kv_heads": Hkv,
                    "head_dim": D, "block_tokens": P, "kv_storage": wl["dtype"], "numerics": args.numerics,
+                   "append": "separate launch" if args.separate_append else "fused into the decode launch",
                    "pool_copies": copies, "parallelism": "single-gpu"},
-        "attention_only": {"tokens_per_s": B / avg_attn_s, "avg_ms": avg_attn_s * 1e3, "median_ms": med_attn_ms,
+        "decode_launch": {"tokens_per_s": B / avg_attn_s, "avg_ms": avg_attn_s * 1e3, "median_ms": med_attn_ms,
                            "p10_ms": attn_ms[len(attn_ms) // 10], "p90_ms": attn_ms[(9 * len(attn_ms)) // 10]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": traffic,

@@ -132,6 +132,17 @@ typedef struct VspecPagedAttnDesc {
 size_t vspec_rocm_paged_decode_workspace_bytes(const VspecPagedAttnDesc* desc);
 int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc);
 
+/* One decode step in one call, the reference step's append + attention pair
+ * (capi.c:2247-2253 -> kv_paged_cache.c:243-310, then cpu_backend.c:40-51 over the
+ * gathered rows): appends one new token per sequence at position ctx_lens[b] - 1 (the
+ * context includes it; a context of 0 appends nothing), exactly as vspec_rocm_kv_append
+ * with start_pos = ctx_lens - 1 and n_new = 1, then attends as
+ * vspec_rocm_paged_decode_attention.  k_new, v_new: device [batch][num_kv_heads][head_dim]
+ * in src_dtype (VSPEC_KV_F32 or VSPEC_KV_F16).  f16 and int4 pools do both in one kernel
+ * launch; f32 pools launch the append first. */
+int vspec_rocm_paged_decode_step(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
+                                 int32_t src_dtype);
+
 /* ---- misc ---- */
 int vspec_rocm_sync(void* stream);
 const char* vspec_rocm_last_error(void);

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from oracle.oracle import DTYPE_F16, DTYPE_F32, DTYPE_INT4, HostPool, _f32p, _u8p, ptr
-from cases import GARBAGE, continuous_c4, make_case, qwen_c2
+from cases import GARBAGE, continuous_c4, fill_garbage, make_case, qwen_c2
 
 pytestmark = pytest.mark.gpu
 TOL = {DTYPE_F32: 1e-4, DTYPE_F16: 4e-3, DTYPE_INT4: 4e-3}
@@ -362,6 +362,75 @@ def test_decode_back_to_back_and_streams(oracle, gpu):
     torch.cuda.synchronize()
     for i, o, _ in outs:
         assert np.array_equal(o.cpu().numpy(), first[i])
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv,D,P,pt", [
+    (DTYPE_F16, 8, 2, 128, 16, 0), (DTYPE_F16, 16, 2, 64, 32, 0), (DTYPE_F16, 32, 8, 128, 16, 32),
+    (DTYPE_INT4, 8, 2, 128, 16, 0), (DTYPE_INT4, 16, 2, 64, 32, 32), (DTYPE_F32, 8, 2, 128, 16, 0)])
+@pytest.mark.parametrize("src16", [False, True])
+def test_decode_step_fused_append(oracle, gpu, dtype, Hq, Hkv, D, P, pt, src16):
+    """vspec_rocm_paged_decode_step (append of the decode token at ctx - 1, then attention;
+    one launch for f16 / int4 pools) against kv_append + paged_decode on a second pool
+    built identically: the same pool bytes and the same outputs bit for bit, both equal to
+    the oracle's append (bit-exact) and attention (within tolerance).  Contexts include 0
+    (nothing appended) and 1 (the new token alone); GQA group 8 makes two q-head groups
+    share each kv head's last tile; P=32 puts two tiles in a block."""
+    import copy
+
+    import torch
+    import vspec_rocm as vr
+
+    say(f"[decode-step] dtype={dtype} Hq={Hq} Hkv={Hkv} D={D} P={P} pt={pt} src16={src16}")
+    ctx = np.array([1, 17, 40, 0, 100, 33, 16], np.int32)
+    full = make_case(oracle, dtype, len(ctx), Hq, Hkv, D, P, ctx, seed=71 + D + P + dtype, src16=src16)
+    pre = [copy.copy(full) for _ in range(2)]
+    pools = []
+    for c in pre:
+        c.ctx = np.maximum(full.ctx - 1, 0).astype(np.int32)
+        c.host = HostPool(dtype, full.num_blocks, P, Hkv, D)
+        fill_garbage(c.host)
+        pools.append(build_both(oracle, c, gpu))
+    host = pre[0].host
+    B = len(ctx)
+    last = np.maximum(ctx - 1, 0)
+    k_new = np.ascontiguousarray(full.k_tokens[np.arange(B), last])  # [B][Hkv][D]
+    v_new = np.ascontiguousarray(full.v_tokens[np.arange(B), last])
+    live = np.flatnonzero(ctx > 0)
+    assert oracle.paged_append(host, np.ascontiguousarray(full.tables[live]), (ctx[live] - 1).astype(np.int32),
+                               np.ascontiguousarray(k_new[live][:, None]), np.ascontiguousarray(v_new[live][:, None]))
+
+    tab = torch.from_numpy(full.tables).to(gpu)
+    cl = torch.from_numpy(ctx).to(gpu)
+    q = torch.from_numpy(full.q).to(gpu)
+    kd, vd = _np_to_dev(k_new, gpu), _np_to_dev(v_new, gpu)
+    # reference flow: separate append launch, then decode
+    vr.kv_append(pools[0], tab, cl - 1, kd[:, None].contiguous(), vd[:, None].contiguous())
+    want = vr.paged_decode(pools[0], tab, cl, q, numerics=1, partition_tokens=pt)
+    got = torch.full_like(q, float("nan"))
+    vr.paged_decode_step(pools[1], tab, cl, q, kd, vd, numerics=1, partition_tokens=pt, out=got)
+    torch.cuda.synchronize()
+    for a, b in zip(pool_bytes(pools[0]), pool_bytes(pools[1])):
+        if a is not None:
+            assert np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+    assert_pools_equal(host, pools[1])
+    assert torch.equal(got, want)
+    full.host = host
+    check_attention(oracle, full, got.cpu().numpy(), 1)
+
+
+def test_decode_step_rejects_bad_source(gpu):
+    import torch
+    import vspec_rocm as vr
+
+    pool = vr.PagedPool(vr.KV_F16, 4, 16, 2, 128, device=gpu)
+    d = vr.make_decode_desc(pool, torch.zeros((1, 4), dtype=torch.int32, device=gpu),
+                            torch.ones(1, dtype=torch.int32, device=gpu), torch.zeros((1, 2, 128), device=gpu),
+                            torch.zeros((1, 2, 128), device=gpu), 1)
+    k = torch.zeros((1, 2, 128), device=gpu)
+    assert vr.lib().vspec_rocm_paged_decode_step(d, k.data_ptr(), None, vr.KV_F32) == 0
+    assert "null" in vr.last_error()
+    assert vr.lib().vspec_rocm_paged_decode_step(d, k.data_ptr(), k.data_ptr(), vr.KV_INT4) == 0
+    assert "src_dtype" in vr.last_error()
 
 
 # ----------------------------------------------------------------------------- config 5

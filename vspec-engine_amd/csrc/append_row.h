@@ -1,0 +1,242 @@
+// append_row.h -- block-table append of one chunk of a token-head row of K or V
+// (kv_paged_cache.c:292-303 in the reference, with quantise-on-write for int4 pools),
+// shared by the append kernels (paged_kv.hip) and the decode kernels' fused decode-step
+// append (decode_mfma.hip, decode_mfma_int4.hip).
+#pragma once
+#include "kv_common.h"
+
+namespace vkv {
+
+struct AppendParams {
+    uint8_t* k;
+    uint8_t* v;
+    uint16_t* ks;
+    uint16_t* vs;
+    const int32_t* block_tables;
+    const int32_t* start_pos;
+    // packed-token mode (token_item != null): source token b (n_new == 1) goes to
+    // position token_pos[b] of block-table row token_item[b]
+    const int32_t* token_item;
+    const int32_t* token_pos;
+    // rotary embedding of K (rope_cos != null): rows [max_pos][rope_dim / 2]
+    const float* rope_cos;
+    const float* rope_sin;
+    uint32_t rope_dim;
+    uint32_t max_pos;
+    // with start_pos and token_item null: source token b goes to position ctx_lens[b] - 1
+    // (the decode step's append; a context of 0 appends nothing)
+    const int32_t* ctx_lens;
+    const uint8_t* k_new;
+    const uint8_t* v_new;
+    uint32_t batch;
+    uint32_t n_new;
+    uint32_t hkv;
+    uint32_t head_dim;
+    uint32_t block_tokens;
+    uint32_t max_blocks;
+    uint32_t num_blocks;
+};
+
+// Elements per append work item: a whole 32-element quantisation group for int4 pools,
+// 8 elements (16 or 32 bytes) otherwise.
+constexpr int append_ept(int dt) { return dt == VSPEC_KV_INT4 ? 32 : 8; }
+
+// Chunk c of the token-head row of K (which 0) or V (which 1) whose first source element
+// is src_el, written at position pos of block-table row `seq`, kv head h.  Positions past
+// the table, behind an invalid entry or (with rotary tables) past max_pos are not written.
+template <int DT, int SRC>
+__device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq, uint32_t pos, uint32_t h,
+                                             uint32_t c, int which, size_t src_el) {
+    constexpr int EPT = append_ept(DT);
+    const uint32_t lb = pos / p.block_tokens;
+    if (lb >= p.max_blocks) return;
+    const int32_t phys = p.block_tables[(size_t)seq * p.max_blocks + lb];
+    if (phys < 0 || (uint32_t)phys >= p.num_blocks) return;
+    const uint32_t slot = pos % p.block_tokens;
+    const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + slot;
+    const size_t e0 = (size_t)c * EPT;  // first element of this chunk within the row
+
+    float x[EPT];
+    const uint8_t* src = which ? p.v_new : p.k_new;
+    if constexpr (SRC == VSPEC_KV_F32) {
+        const float4* s4 = reinterpret_cast<const float4*>(src + src_el * 4);
+#pragma unroll
+        for (int j = 0; j < EPT / 4; ++j) {
+            const float4 w = s4[j];
+            x[4 * j] = w.x; x[4 * j + 1] = w.y; x[4 * j + 2] = w.z; x[4 * j + 3] = w.w;
+        }
+    } else {
+        const uint4* s4 = reinterpret_cast<const uint4*>(src + src_el * 2);
+#pragma unroll
+        for (int j = 0; j < EPT / 8; ++j) unpack_f16x8(s4[j], x + 8 * j);
+    }
+    const bool rope = p.rope_cos != nullptr;
+    if (rope) {
+        if (pos >= p.max_pos) return;  // no table row: the token is not written
+        if (!which) {
+#pragma clang fp contract(off)
+            // pairs (i, i + half) of the first rope_dim elements rotate by row `pos`:
+            // x1*c - x2*s, x1*s + x2*c, each product and sum rounded separately (no
+            // fused multiply-add: hipcc contracts by default)
+            const uint32_t half = p.rope_dim / 2;
+            const size_t row0 = src_el - e0;  // element 0 of this token-head row
+            const float* cr = p.rope_cos + (size_t)pos * half;
+            const float* sr = p.rope_sin + (size_t)pos * half;
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+                const uint32_t d = (uint32_t)e0 + e;
+                if (d >= p.rope_dim) continue;
+                const uint32_t i = d < half ? d : d - half;
+                const size_t pe = row0 + (d < half ? d + half : d - half);
+                float other;
+                if constexpr (SRC == VSPEC_KV_F32) {
+                    other = reinterpret_cast<const float*>(src)[pe];
+                } else {
+                    other = half_bits_to_float(reinterpret_cast<const uint16_t*>(src)[pe]);
+                }
+                const float c = cr[i], sn = sr[i];
+                x[e] = d < half ? x[e] * c - other * sn : other * sn + x[e] * c;
+            }
+        }
+    }
+
+    uint8_t* dst = which ? p.v : p.k;
+    if constexpr (DT == VSPEC_KV_F32) {
+        float4* d4 = reinterpret_cast<float4*>(dst + (row * p.head_dim + e0) * 4);
+        d4[0] = make_float4(x[0], x[1], x[2], x[3]);
+        d4[1] = make_float4(x[4], x[5], x[6], x[7]);
+    } else if constexpr (DT == VSPEC_KV_F16) {
+        uint32_t hb[8];
+        if (SRC == VSPEC_KV_F16 && !(rope && !which)) {
+            // pure copy of the source bits
+            const uint4 w = *reinterpret_cast<const uint4*>(src + src_el * 2);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                hb[2 * k] = ws[k] & 0xffffu;
+                hb[2 * k + 1] = ws[k] >> 16;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) hb[k] = float_to_half_bits(x[k]);
+        }
+        if (which) {
+            // V tiles are d-major: element (d, slot) at tile + d*P + slot
+            uint16_t* vt = reinterpret_cast<uint16_t*>(dst) +
+                           ((size_t)phys * p.hkv + h) * p.head_dim * p.block_tokens + slot;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) vt[(e0 + k) * p.block_tokens] = (uint16_t)hb[k];
+        } else {
+            *reinterpret_cast<uint4*>(dst + (row * p.head_dim + e0) * 2) =
+                make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16),
+                           hb[6] | (hb[7] << 16));
+        }
+    } else {
+        // int4 codec: rep = 2nd-largest |x|, scale = rep/8 (1 if rep == 0),
+        // floored at 1e-6, rounded to fp16 (saturating), codes rint(x/scale) in [-8,7]
+        float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float a = fabsf(x[e]);
+            if (a > a1) {
+                a2 = a1;
+                a1 = a;
+            } else if (a > a2) {
+                a2 = a;
+            }
+        }
+        float scale = a2 > 0.f ? a2 / 8.0f : 1.0f;
+        if (scale < 1e-6f) scale = 1e-6f;
+        uint32_t s16 = float_to_half_bits(scale);
+        if ((s16 & 0x7fffu) >= 0x7c00u) s16 = 0x7bffu;
+        const float sc = half_bits_to_float(s16);
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float rr = rintf(x[e] / sc);
+            const int code = rr > 7.0f ? 7 : (rr >= -8.0f ? (int)rr : -8);
+            w[e / 8] |= ((uint32_t)code & 0xfu) << (4 * (e % 8));
+        }
+        const size_t bh = (size_t)phys * p.hkv + h;
+        if (which) {
+            // V tiles: byte n of this group's 16 holds d = 32c + n (low nibble) and
+            // d = 32c + 16 + n (high nibble) of this token, at lane chunk (g, n)
+            const uint32_t tt = slot & 15u, tg = tt >> 2, tr = tt & 3u;
+            uint8_t* vb = dst + bh * ((size_t)p.block_tokens * p.head_dim / 2) +
+                          (size_t)(slot >> 4) * (8u * p.head_dim) + (size_t)(16u * tg) * (p.head_dim / 8u) +
+                          4u * c + 2u * (tr & 1u) + (tr >> 1);
+#pragma unroll
+            for (int nn = 0; nn < 16; ++nn) {
+                const uint32_t lo = (w[nn / 8] >> (4 * (nn % 8))) & 0xfu;
+                const uint32_t hi = (w[2 + nn / 8] >> (4 * (nn % 8))) & 0xfu;
+                vb[(size_t)nn * (p.head_dim / 8u)] = (uint8_t)(lo | (hi << 4));
+            }
+            p.vs[row * (p.head_dim / 32) + c] = (uint16_t)s16;
+        } else {
+            uint4* d4 = reinterpret_cast<uint4*>(dst + row * (p.head_dim / 2) + e0 / 2);
+            *d4 = make_uint4(w[0], w[1], w[2], w[3]);
+            p.ks[int4_ks_index(bh, p.head_dim / 32, p.block_tokens, slot, c)] = (uint16_t)s16;
+        }
+    }
+}
+
+// Fused decode-step append of the MFMA decode kernels (p.k_new != null).  Every work
+// item whose last tile lies in this workgroup's range [ws.lo, ws.hi) -- exactly one
+// workgroup per work item -- gets its sequence's new token written for its kv head at
+// position ctx_lens[b] - 1, exactly as the append kernel writes it.  All threads call this
+// before the workgroup reads any tile; it returns with the stores complete and a barrier
+// passed, so the workgroup's later loads of those tiles see them.  Other workgroups never
+// read the rows written here (they belong to the item's last tile), except the owners of
+// the other q-head groups of the same kv head, which write the same bytes themselves.
+template <int DT, int D>
+__device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCursor c, const int ips) {
+    constexpr int EPT = append_ept(DT);
+    constexpr int kItems = D / EPT * 2;  // append work items per token-head row (K and V)
+    static_assert(kItems <= kWaves * 64, "one pass of the workgroup's threads");
+    AppendParams a;
+    a.k = const_cast<uint8_t*>(p.k);
+    a.v = const_cast<uint8_t*>(p.v);
+    a.ks = const_cast<uint16_t*>(p.ks);
+    a.vs = const_cast<uint16_t*>(p.vs);
+    a.block_tables = p.block_tables;
+    a.start_pos = nullptr;
+    a.token_item = nullptr;
+    a.token_pos = nullptr;
+    a.rope_cos = nullptr;
+    a.rope_sin = nullptr;
+    a.rope_dim = 0;
+    a.max_pos = 0;
+    a.ctx_lens = p.ctx_lens;
+    a.k_new = p.k_new;
+    a.v_new = p.v_new;
+    a.batch = p.batch;
+    a.n_new = 1;
+    a.hkv = p.hkv;
+    a.head_dim = D;
+    a.block_tokens = p.block_tokens;
+    a.max_blocks = p.max_blocks;
+    a.num_blocks = p.num_blocks;
+    const int t = (int)threadIdx.x;
+    while (true) {
+        const int last = c.item0 + c.U - 1;
+        if (last >= ws.lo && last < ws.hi) {
+            const int ctx = as_const(p.ctx_lens)[c.b];
+            if (ctx > 0 && t < kItems) {
+                const uint32_t hk = (uint32_t)c.y / p.gsplit;
+                const uint32_t ch = (uint32_t)t >> 1;
+                const size_t src_el = ((size_t)c.b * p.hkv + hk) * D + (size_t)ch * EPT;
+                if (p.append_src == VSPEC_KV_F32) {
+                    append_chunk<DT, VSPEC_KV_F32>(a, (uint32_t)c.b, (uint32_t)ctx - 1u, hk, ch, t & 1, src_el);
+                } else {
+                    append_chunk<DT, VSPEC_KV_F16>(a, (uint32_t)c.b, (uint32_t)ctx - 1u, hk, ch, t & 1, src_el);
+                }
+            }
+        }
+        if (c.item0 + c.U >= ws.hi) break;
+        cursor_next(p, ips, c);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
+    __syncthreads();
+}
+
+}  // namespace vkv

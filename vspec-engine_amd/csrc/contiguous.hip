@@ -265,10 +265,10 @@ int side_to_device(const VspecKVCache* c, const CacheSide& s, float* d_rows) {
         const size_t n = rows * c->head_dim;
         const unsigned grid = (unsigned)((n + kThreads - 1) / kThreads < 8192 ? (n + kThreads - 1) / kThreads : 8192);
         hipLaunchKernelGGL(int3_rows_to_f32, dim3(grid), dim3(kThreads), 0, nullptr, p);
-        ok = hipGetLastError() == hipSuccess;
-        if (!ok) vspec_rocm_set_error_("attention: int3 decode launch failed");
+        ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(nullptr) == hipSuccess;
+        if (!ok) vspec_rocm_set_error_("attention: int3 decode failed");
     }
-    (void)hipFree(d_codes);  // synchronises with the decode kernel
+    (void)hipFree(d_codes);
     (void)hipFree(d_scales);
     return ok;
 }

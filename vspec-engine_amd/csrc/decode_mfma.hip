@@ -15,6 +15,7 @@
 // The std clamp is screened per key from v_dot2 sums (sum x, sum x^2) and a packed
 // max|x|; keys it may affect (about 0.1% for N(0,1) data) get their scores recomputed
 // exactly in fp32 from the clipped row, replacing the MFMA value.
+#include "append_row.h"
 #include "kv_common.h"
 
 namespace vkv {
@@ -73,6 +74,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const WorkSplit ws = work_split(p, ips, split_sh);
     if (ws.lo >= ws.hi) return;
     const ItemCursor first = cursor_at(p, ws);
+    if (p.k_new) fused_append<VSPEC_KV_F16, D>(p, ws, first, ips);
 
 
     // ---- q' = clip(q) * scale * log2(e) of work item c (segment s) for this wave, and

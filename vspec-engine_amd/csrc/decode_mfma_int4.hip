@@ -22,6 +22,7 @@
 //
 // The std clamp is screened per key from v_dot8 sums of the codes (sum c, sum c^2)
 // and the bound |x| <= 8 * scale; keys it may affect get exact fp32 scores.
+#include "append_row.h"
 #include "kv_common.h"
 
 namespace vkv {
@@ -88,6 +89,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 
     const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
     const WorkSplit ws = work_split(p, ips, split_sh);
+    if (p.k_new && ws.lo < ws.hi) fused_append<VSPEC_KV_INT4, D>(p, ws, cursor_at(p, ws), ips);
     int b = ws.b;
     int seq0 = ws.seq0;
     for (int pos = ws.lo; pos < ws.hi;) {
@@ -436,7 +438,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 }
 
 #ifndef VSPEC_I4_PAIRS_IN_FLIGHT
-#define VSPEC_I4_PAIRS_IN_FLIGHT 2
+#define VSPEC_I4_PAIRS_IN_FLIGHT 1
 #endif
 
 template <int D, int GW>

@@ -191,6 +191,12 @@ struct DecodeParams {
     uint32_t batch;
     uint32_t max_tiles;    // tiles of the host's context bound (max_ctx_len)
     uint32_t chunk_tiles;  // tiles per workgroup, or 0: split evenly over gridDim.x
+    // fused decode-step append of the MFMA kernels (k_new != null): each sequence's new
+    // token, [batch][hkv][D] in append_src (VSPEC_KV_F32 / VSPEC_KV_F16), is written at
+    // position ctx_lens[b] - 1 before any tile is read
+    const uint8_t* k_new;
+    const uint8_t* v_new;
+    int32_t append_src;
 };
 
 

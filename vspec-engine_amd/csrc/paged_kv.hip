@@ -47,6 +47,7 @@ extern "C" void vspec_rocm_set_error_(const char* msg) { set_err("%s", msg ? msg
     } while (0)
 
 #include "kv_common.h"
+#include "append_row.h"
 
 namespace {
 using namespace vkv;
@@ -355,38 +356,11 @@ __global__ __launch_bounds__(D) void decode_combine(DecodeParams p) {
 // ---------------------------------------------------------------------------
 // append (quantise-on-write for int4)
 // ---------------------------------------------------------------------------
-struct AppendParams {
-    uint8_t* k;
-    uint8_t* v;
-    uint16_t* ks;
-    uint16_t* vs;
-    const int32_t* block_tables;
-    const int32_t* start_pos;
-    // packed-token mode (token_item != null): source token b (n_new == 1) goes to
-    // position token_pos[b] of block-table row token_item[b]
-    const int32_t* token_item;
-    const int32_t* token_pos;
-    // rotary embedding of K (rope_cos != null): rows [max_pos][rope_dim / 2]
-    const float* rope_cos;
-    const float* rope_sin;
-    uint32_t rope_dim;
-    uint32_t max_pos;
-    const uint8_t* k_new;
-    const uint8_t* v_new;
-    uint32_t batch;
-    uint32_t n_new;
-    uint32_t hkv;
-    uint32_t head_dim;
-    uint32_t block_tokens;
-    uint32_t max_blocks;
-    uint32_t num_blocks;
-};
-
 // One work item = EPT consecutive elements of one token-head row of K or V: a whole
 // 32-element quantisation group for int4 pools, 8 elements (16 or 32 bytes) otherwise.
 template <int DT, int SRC>
 __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
-    constexpr int EPT = DT == VSPEC_KV_INT4 ? 32 : 8;
+    constexpr int EPT = append_ept(DT);
     const uint32_t chunks = p.head_dim / EPT;
     const uint64_t total = (uint64_t)p.batch * p.n_new * p.hkv * chunks * 2;
     for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
@@ -400,141 +374,19 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
         const uint32_t i = (uint32_t)(r % p.n_new);
         const uint32_t b = (uint32_t)(r / p.n_new);
 
-        const uint32_t seq = p.token_item ? (uint32_t)p.token_item[b] : b;
-        const int32_t sp = p.token_item ? p.token_pos[b] : p.start_pos[b];
-        if (sp < 0 || (p.token_item && p.token_item[b] < 0)) continue;
-        const uint32_t pos = (uint32_t)sp + i;
-        const uint32_t lb = pos / p.block_tokens;
-        if (lb >= p.max_blocks) continue;
-        const int32_t phys = p.block_tables[(size_t)seq * p.max_blocks + lb];
-        if (phys < 0 || (uint32_t)phys >= p.num_blocks) continue;
-        const uint32_t slot = pos % p.block_tokens;
-        const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + slot;
-        const size_t e0 = (size_t)c * EPT;  // first element of this chunk within the row
-        const size_t src_el = (((size_t)b * p.n_new + i) * p.hkv + h) * p.head_dim + e0;
-
-        float x[EPT];
-        const uint8_t* src = which ? p.v_new : p.k_new;
-        if constexpr (SRC == VSPEC_KV_F32) {
-            const float4* s4 = reinterpret_cast<const float4*>(src + src_el * 4);
-#pragma unroll
-            for (int j = 0; j < EPT / 4; ++j) {
-                const float4 w = s4[j];
-                x[4 * j] = w.x; x[4 * j + 1] = w.y; x[4 * j + 2] = w.z; x[4 * j + 3] = w.w;
-            }
+        const int32_t item = p.token_item ? p.token_item[b] : (int32_t)b;
+        int32_t sp;
+        if (p.token_item) {
+            sp = p.token_pos[b];
+        } else if (p.start_pos) {
+            sp = p.start_pos[b];
         } else {
-            const uint4* s4 = reinterpret_cast<const uint4*>(src + src_el * 2);
-#pragma unroll
-            for (int j = 0; j < EPT / 8; ++j) unpack_f16x8(s4[j], x + 8 * j);
+            const int32_t cl = p.ctx_lens[b];
+            sp = cl > 0 ? cl - 1 : -1;
         }
-        const bool rope = p.rope_cos != nullptr;
-        if (rope) {
-            if (pos >= p.max_pos) continue;  // no table row: the token is not written
-            if (!which) {
-#pragma clang fp contract(off)
-                // pairs (i, i + half) of the first rope_dim elements rotate by row `pos`:
-                // x1*c - x2*s, x1*s + x2*c, each product and sum rounded separately (no
-                // fused multiply-add: hipcc contracts by default)
-                const uint32_t half = p.rope_dim / 2;
-                const size_t row0 = src_el - e0;  // element 0 of this token-head row
-                const float* cr = p.rope_cos + (size_t)pos * half;
-                const float* sr = p.rope_sin + (size_t)pos * half;
-#pragma unroll
-                for (int e = 0; e < EPT; ++e) {
-                    const uint32_t d = (uint32_t)e0 + e;
-                    if (d >= p.rope_dim) continue;
-                    const uint32_t i = d < half ? d : d - half;
-                    const size_t pe = row0 + (d < half ? d + half : d - half);
-                    float other;
-                    if constexpr (SRC == VSPEC_KV_F32) {
-                        other = reinterpret_cast<const float*>(src)[pe];
-                    } else {
-                        other = half_bits_to_float(reinterpret_cast<const uint16_t*>(src)[pe]);
-                    }
-                    const float c = cr[i], sn = sr[i];
-                    x[e] = d < half ? x[e] * c - other * sn : other * sn + x[e] * c;
-                }
-            }
-        }
-
-        uint8_t* dst = which ? p.v : p.k;
-        if constexpr (DT == VSPEC_KV_F32) {
-            float4* d4 = reinterpret_cast<float4*>(dst + (row * p.head_dim + e0) * 4);
-            d4[0] = make_float4(x[0], x[1], x[2], x[3]);
-            d4[1] = make_float4(x[4], x[5], x[6], x[7]);
-        } else if constexpr (DT == VSPEC_KV_F16) {
-            uint32_t hb[8];
-            if (SRC == VSPEC_KV_F16 && !(rope && !which)) {
-                // pure copy of the source bits
-                const uint4 w = *reinterpret_cast<const uint4*>(src + src_el * 2);
-                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    hb[2 * k] = ws[k] & 0xffffu;
-                    hb[2 * k + 1] = ws[k] >> 16;
-                }
-            } else {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) hb[k] = float_to_half_bits(x[k]);
-            }
-            if (which) {
-                // V tiles are d-major: element (d, slot) at tile + d*P + slot
-                uint16_t* vt = reinterpret_cast<uint16_t*>(dst) +
-                               ((size_t)phys * p.hkv + h) * p.head_dim * p.block_tokens + slot;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) vt[(e0 + k) * p.block_tokens] = (uint16_t)hb[k];
-            } else {
-                *reinterpret_cast<uint4*>(dst + (row * p.head_dim + e0) * 2) =
-                    make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16),
-                               hb[6] | (hb[7] << 16));
-            }
-        } else {
-            // int4 codec: rep = 2nd-largest |x|, scale = rep/8 (1 if rep == 0),
-            // floored at 1e-6, rounded to fp16 (saturating), codes rint(x/scale) in [-8,7]
-            float a1 = 0.f, a2 = 0.f;
-#pragma unroll
-            for (int e = 0; e < 32; ++e) {
-                const float a = fabsf(x[e]);
-                if (a > a1) {
-                    a2 = a1;
-                    a1 = a;
-                } else if (a > a2) {
-                    a2 = a;
-                }
-            }
-            float scale = a2 > 0.f ? a2 / 8.0f : 1.0f;
-            if (scale < 1e-6f) scale = 1e-6f;
-            uint32_t s16 = float_to_half_bits(scale);
-            if ((s16 & 0x7fffu) >= 0x7c00u) s16 = 0x7bffu;
-            const float sc = half_bits_to_float(s16);
-            uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int e = 0; e < 32; ++e) {
-                const float rr = rintf(x[e] / sc);
-                const int code = rr > 7.0f ? 7 : (rr >= -8.0f ? (int)rr : -8);
-                w[e / 8] |= ((uint32_t)code & 0xfu) << (4 * (e % 8));
-            }
-            const size_t bh = (size_t)phys * p.hkv + h;
-            if (which) {
-                // V tiles: byte n of this group's 16 holds d = 32c + n (low nibble) and
-                // d = 32c + 16 + n (high nibble) of this token, at lane chunk (g, n)
-                const uint32_t tt = slot & 15u, tg = tt >> 2, tr = tt & 3u;
-                uint8_t* vb = dst + bh * ((size_t)p.block_tokens * p.head_dim / 2) +
-                              (size_t)(slot >> 4) * (8u * p.head_dim) + (size_t)(16u * tg) * (p.head_dim / 8u) +
-                              4u * c + 2u * (tr & 1u) + (tr >> 1);
-#pragma unroll
-                for (int nn = 0; nn < 16; ++nn) {
-                    const uint32_t lo = (w[nn / 8] >> (4 * (nn % 8))) & 0xfu;
-                    const uint32_t hi = (w[2 + nn / 8] >> (4 * (nn % 8))) & 0xfu;
-                    vb[(size_t)nn * (p.head_dim / 8u)] = (uint8_t)(lo | (hi << 4));
-                }
-                p.vs[row * (p.head_dim / 32) + c] = (uint16_t)s16;
-            } else {
-                uint4* d4 = reinterpret_cast<uint4*>(dst + row * (p.head_dim / 2) + e0 / 2);
-                *d4 = make_uint4(w[0], w[1], w[2], w[3]);
-                p.ks[int4_ks_index(bh, p.head_dim / 32, p.block_tokens, slot, c)] = (uint16_t)s16;
-            }
-        }
+        if (sp < 0 || item < 0) continue;
+        const size_t src_el = (((size_t)b * p.n_new + i) * p.hkv + h) * p.head_dim + (size_t)c * EPT;
+        append_chunk<DT, SRC>(p, (uint32_t)item, (uint32_t)sp + i, h, c, which, src_el);
     }
 }
 
@@ -1390,7 +1242,13 @@ size_t vspec_rocm_paged_decode_workspace_bytes(const VspecPagedAttnDesc* desc) {
     return pl.ws_bytes;
 }
 
-int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
+}  // extern "C"
+
+namespace {
+
+// Decode attention, with the decode step's append of k_new / v_new first when they are
+// given (one launch for the f16 and int4 kernels, an append launch before the f32 one).
+int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new, int32_t src_dtype) {
     if (!desc) {
         set_err("paged_decode: null descriptor");
         return 0;
@@ -1459,8 +1317,35 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
     p.batch = desc->batch;
     p.max_tiles = pl.max_tiles;
     p.chunk_tiles = pl.chunk_tiles;
+    p.k_new = nullptr;
+    p.v_new = nullptr;
+    p.append_src = src_dtype;
 
     hipStream_t s = (hipStream_t)desc->stream;
+    if (k_new) {
+        if (pl.split) {
+            p.k_new = (const uint8_t*)k_new;
+            p.v_new = (const uint8_t*)v_new;
+        } else {
+            AppendParams a = {};
+            a.k = (uint8_t*)desc->kv.k_data;
+            a.v = (uint8_t*)desc->kv.v_data;
+            a.ks = desc->kv.k_scales;
+            a.vs = desc->kv.v_scales;
+            a.block_tables = desc->block_tables;
+            a.ctx_lens = desc->ctx_lens;
+            a.k_new = (const uint8_t*)k_new;
+            a.v_new = (const uint8_t*)v_new;
+            a.batch = desc->batch;
+            a.n_new = 1;
+            a.hkv = desc->kv.num_kv_heads;
+            a.head_dim = desc->kv.head_dim;
+            a.block_tokens = desc->kv.block_tokens;
+            a.max_blocks = desc->max_blocks_per_seq;
+            a.num_blocks = desc->kv.num_blocks;
+            if (!append_launch("paged_decode_step append launch", &desc->kv, a, src_dtype, s)) return 0;
+        }
+    }
     if (pl.split) {
         // partial slots [grid][2][GW] of (max, sum) then of acc[D]
         p.part_acc = (float*)ws + (size_t)pl.grid_x * 2 * pl.gw * 2;
@@ -1486,6 +1371,27 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
         HIP_CHECK(hipGetLastError(), "decode_combine launch");
     }
     return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
+    return paged_decode(desc, nullptr, nullptr, VSPEC_KV_F32);
+}
+
+int vspec_rocm_paged_decode_step(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
+                                 int32_t src_dtype) {
+    if (!k_new || !v_new) {
+        set_err("paged_decode_step: null k_new or v_new");
+        return 0;
+    }
+    if (src_dtype != VSPEC_KV_F32 && src_dtype != VSPEC_KV_F16) {
+        set_err("paged_decode_step: src_dtype must be f32 or f16");
+        return 0;
+    }
+    return paged_decode(desc, k_new, v_new, src_dtype);
 }
 
 }  // extern "C"

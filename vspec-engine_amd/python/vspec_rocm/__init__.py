@@ -154,6 +154,7 @@ SIGNATURES = {
     "vspec_rocm_kv_compact": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp]),
     "vspec_rocm_paged_decode_workspace_bytes": (C.c_size_t, [C.POINTER(VspecPagedAttnDesc)]),
     "vspec_rocm_paged_decode_attention": (C.c_int, [C.POINTER(VspecPagedAttnDesc)]),
+    "vspec_rocm_paged_decode_step": (C.c_int, [C.POINTER(VspecPagedAttnDesc), _vp, _vp, C.c_int32]),
     "vspec_rocm_sync": (C.c_int, [_vp]),
     "vspec_rocm_last_error": (C.c_char_p, []),
     "vspec_rocm_device_count": (C.c_int, []),
@@ -407,6 +408,29 @@ def paged_decode(pool: PagedPool, block_tables, ctx_lens, q, max_ctx_len=None, n
         out = torch.empty_like(q)
     d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream)
     _check(lib().vspec_rocm_paged_decode_attention(C.byref(d)), "paged_decode_attention")
+    return out
+
+
+def paged_decode_step(pool: PagedPool, block_tables, ctx_lens, q, k_new, v_new, max_ctx_len=None,
+                      numerics=NUMERICS_PLAIN, scale=0.0, partition_tokens=0, out=None, workspace=None,
+                      stream=None):
+    """vspec_rocm_paged_decode_step: append k_new / v_new [B][Hkv][D] (float32 or float16,
+    device) at position ctx_lens[b] - 1, then decode q [B][Hq][D] float32 -> out."""
+    import torch
+
+    assert q.dtype == torch.float32 and q.is_contiguous()
+    assert k_new.is_contiguous() and v_new.is_contiguous() and k_new.shape == v_new.shape
+    assert k_new.dtype in (torch.float32, torch.float16) and v_new.dtype == k_new.dtype
+    src = KV_F32 if k_new.dtype == torch.float32 else KV_F16
+    bt = block_tables.to(torch.int32).contiguous()
+    cl = ctx_lens.to(torch.int32).contiguous()
+    if max_ctx_len is None:
+        max_ctx_len = int(cl.max().item()) if cl.numel() else 0
+    if out is None:
+        out = torch.empty_like(q)
+    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream)
+    _check(lib().vspec_rocm_paged_decode_step(C.byref(d), k_new.data_ptr(), v_new.data_ptr(), src),
+           "paged_decode_step")
     return out
 
 
