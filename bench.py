@@ -297,13 +297,16 @@ def run_c5(args, wl, kv_dtype, mode):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="qwen3-8b-b64-ctx4k", choices=sorted(WORKLOADS))
     ap.add_argument("--numerics", default="R", choices=["P", "R"])
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--cpu-seqs", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--event-every", type=int, default=4,
+                    help="bracket every Nth timed launch with a HIP event pair (each pair adds ~7 us "
+                         "to its step); the roofline averages the bracketed launches")
     ap.add_argument("--separate-append", action="store_true",
                     help="append with its own launch before the decode launch (timed: the decode)")
     ap.add_argument("--seed", type=int, default=2026)
@@ -393,11 +396,13 @@ def main():
         d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
     L = vr.lib()
 
+    every = max(1, args.event_every)
+
     def step(i):
         c = i % copies
         if args.separate_append:
             vr.kv_append(pools[c], tables_l[c], pos, k_new, v_new)
-        ev = evs[i] if i >= 0 else None
+        ev = evs[i // every] if i >= 0 and i % every == 0 else None
         if ev:
             ev[0].record()
         if args.separate_append:
@@ -414,7 +419,8 @@ def main():
     for i in range(args.warmup):
         step(-1 - i)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range((args.steps + every - 1) // every)]
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(i)
@@ -449,7 +455,8 @@ def main():
                    "head_dim": D, "block_tokens": P, "kv_storage": wl["dtype"], "numerics": args.numerics,
                    "append": "separate launch" if args.separate_append else "fused into the decode launch",
                    "pool_copies": copies, "parallelism": "single-gpu"},
-        "decode_launch": {"tokens_per_s": B / avg_attn_s, "avg_ms": avg_attn_s * 1e3, "median_ms": med_attn_ms,
+        "decode_launch": {"launches_timed": len(attn_ms), "every": every,
+                          "tokens_per_s": B / avg_attn_s, "avg_ms": avg_attn_s * 1e3, "median_ms": med_attn_ms,
                            "p10_ms": attn_ms[len(attn_ms) // 10], "p90_ms": attn_ms[(9 * len(attn_ms)) // 10]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": traffic,

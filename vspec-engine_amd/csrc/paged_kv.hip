@@ -702,16 +702,20 @@ int check_kv(const VspecPagedKV* kv, const char* who, bool decode = false) {
     return 1;
 }
 
-// grow-only library workspace per device (used when the caller passes none)
+// grow-only library workspace per device (used when the caller passes none); the mutex
+// keeps host threads that decode on one device from growing it at the same time (its
+// contents are shared: concurrent decodes need workspaces of their own)
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
 Workspace g_ws[64];
+std::mutex g_ws_mu;
 
 void* library_workspace(size_t bytes) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace& w = g_ws[dev];
     if (w.bytes >= bytes) return w.ptr;
     if (w.ptr) (void)hipFree(w.ptr);
