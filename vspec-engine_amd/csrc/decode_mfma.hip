@@ -152,10 +152,10 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         const int slot0 = (tile % tiles_per_block) * kTile;
         const uint4* kr = reinterpret_cast<const uint4*>(kbase + (tidx * P + slot0 + n) * D + 8 * g);
 #pragma unroll
-        for (int i = 0; i < NQK; ++i) f.k[i] = kr[4 * i];
+        for (int i = 0; i < NQK; ++i) f.k[i] = load_stream4(kr + 4 * i);
         const _Float16* vt = vbase + tidx * (size_t)D * P + slot0 + 4 * g;
 #pragma unroll
-        for (int j = 0; j < NDT; ++j) f.v[j] = *reinterpret_cast<const uint2*>(vt + (size_t)(16 * j + n) * P);
+        for (int j = 0; j < NDT; ++j) f.v[j] = load_stream2(vt + (size_t)(16 * j + n) * P);
         return ok;
     };
 

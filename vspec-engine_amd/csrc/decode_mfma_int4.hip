@@ -176,22 +176,22 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             const uint8_t* kr = p.k + (bh * P + slot0 + n) * (D / 2) + 4 * g * NQ;
             const uint8_t* vc = p.v + bh * ((size_t)P * D / 2) + (size_t)(slot0 / kTile) * (8 * D) + (16 * g + n) * (D / 8);
             if constexpr (NQ == 4) {
-                const uint4 a = *reinterpret_cast<const uint4*>(kr);
-                const uint4 c = *reinterpret_cast<const uint4*>(vc);
+                const uint4 a = load_stream4(kr);
+                const uint4 c = load_stream4(vc);
                 f.k[0] = a.x; f.k[1] = a.y; f.k[2] = a.z; f.k[3] = a.w;
                 f.v[0] = c.x; f.v[1] = c.y; f.v[2] = c.z; f.v[3] = c.w;
             } else {
-                const uint2 a = *reinterpret_cast<const uint2*>(kr);
-                const uint2 c = *reinterpret_cast<const uint2*>(vc);
+                const uint2 a = load_stream2(kr);
+                const uint2 c = load_stream2(vc);
                 f.k[0] = a.x; f.k[1] = a.y;
                 f.v[0] = c.x; f.v[1] = c.y;
             }
-            f.ks_own = p.ks[(bh * NG + own_group) * P + slot0 + n];
-            f.ks_col = *reinterpret_cast<const uint2*>(p.ks + (bh * NG + col_group) * P + slot0 + 4 * g);
+            f.ks_own = load_stream_u16(p.ks + (bh * NG + own_group) * P + slot0 + n);
+            f.ks_col = load_stream2(p.ks + (bh * NG + col_group) * P + slot0 + 4 * g);
             const uint4* vs = reinterpret_cast<const uint4*>(p.vs + (bh * P + slot0 + 4 * g) * NG);
 #pragma unroll
             for (int i = 0; i < NQ / 2; ++i) {
-                const uint4 w = vs[i];
+                const uint4 w = load_stream4(vs + i);
                 f.vs[4 * i] = w.x; f.vs[4 * i + 1] = w.y; f.vs[4 * i + 2] = w.z; f.vs[4 * i + 3] = w.w;
             }
             return ok;
