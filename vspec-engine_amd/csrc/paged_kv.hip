@@ -624,8 +624,10 @@ __global__ __launch_bounds__(256) void kv_compact(CompactParams p) {
          j += (uint64_t)gridDim.x * blockDim.x) {
         uint8_t* base = j < n16 ? p.k : p.v;
         const uint64_t jj = j < n16 ? j : j - n16;
-        reinterpret_cast<uint4*>(base + (uint64_t)d * p.block_bytes)[jj] =
-            reinterpret_cast<const uint4*>(base + (uint64_t)s * p.block_bytes)[jj];
+        // each byte moves once: streaming (non-temporal) load and store
+        const uint4 w = load_stream4(reinterpret_cast<const uint4*>(base + (uint64_t)s * p.block_bytes) + jj);
+        nt_u32x4 wv = {w.x, w.y, w.z, w.w};
+        __builtin_nontemporal_store(wv, reinterpret_cast<nt_u32x4*>(base + (uint64_t)d * p.block_bytes) + jj);
     }
     if (p.block_scales) {
         for (uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; j < 2 * p.block_scales;
