@@ -293,6 +293,43 @@ def test_config4_continuous_batching(oracle, gpu):
         check_attention(oracle, case, got, 0, subset=subset)
 
 
+def test_decode_uneven_pair_shares(oracle, gpu):
+    """With a grid of two workgroups per CU and a ragged f16 batch, the balanced split
+    gives the first-half workgroup of each pair a larger share of the tiles (the CU's
+    arbiter favours its older waves).  Every share the library accepts (500..900 per mille,
+    VSPEC_ROCM_DECODE_OLD_PERMILLE) changes the rounding only: the outputs stay within
+    tolerance of the oracle and within 1e-5 of the equal split, every row written."""
+    import os
+
+    import torch
+    import vspec_rocm as vr
+
+    say("[pair shares] build")
+    ctx = oracle.uniform_int(91, 3000, 5200, 20)
+    case = make_case(oracle, DTYPE_F16, 20, 32, 8, 128, 16, ctx, seed=92)
+    pool = build_both(oracle, case, gpu, prefix_split=False)
+    tab = torch.from_numpy(case.tables).to(gpu)
+    cl = torch.from_numpy(case.ctx).to(gpu)
+    q = torch.from_numpy(case.q).to(gpu)
+    outs = {}
+    old = os.environ.get("VSPEC_ROCM_DECODE_OLD_PERMILLE")
+    try:
+        for pm in (500, 620, 700, 900):
+            os.environ["VSPEC_ROCM_DECODE_OLD_PERMILLE"] = str(pm)
+            out = torch.full_like(q, float("nan"))
+            vr.paged_decode(pool, tab, cl, q, max_ctx_len=case.tmax, numerics=1, out=out)
+            outs[pm] = out.cpu().numpy()
+    finally:
+        if old is None:
+            os.environ.pop("VSPEC_ROCM_DECODE_OLD_PERMILLE", None)
+        else:
+            os.environ["VSPEC_ROCM_DECODE_OLD_PERMILLE"] = old
+    for pm, o in outs.items():
+        assert np.isfinite(o).all(), pm
+        assert np.abs(o - outs[500]).max() < 1e-5, pm
+    check_attention(oracle, case, outs[700], 1, subset=[0, 5, 11, 19])
+
+
 def test_decode_partition_invariance(oracle, gpu):
     """Split-K partition size changes rounding only."""
     say("[partitions]")

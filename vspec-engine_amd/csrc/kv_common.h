@@ -213,8 +213,10 @@ struct DecodeParams {
     const uint8_t* k_new;
     const uint8_t* v_new;
     int32_t append_src;
+    // balanced split with a grid of two workgroups per CU: share of the first-half
+    // workgroup of each (g, g + G/2) pair in 1/1000 (500: equal shares)
+    uint32_t split_old_permille;
 };
-
 
 // Launch the MFMA decode kernels for f16 pools (decode_mfma.hip) and int4 pools
 // (decode_mfma_int4.hip); they return 0 when no instantiation matches (head_dim,
@@ -285,6 +287,9 @@ __device__ __forceinline__ const const_i32* as_const(const int32_t* ptr) { retur
 struct WorkSplit {
     int total;   // T
     int groups;  // G (balanced split), 0 for the chunked split
+    int half;    // G / 2 when the two halves of the grid get different shares, else 0
+    int wa;      // share of a first-half workgroup in a (first, second) pair, in 1/1000
+    int ragged;  // the sequences' contexts differ in tiles
     int lo, hi;  // this workgroup's tiles
     int b;       // sequence holding tile lo
     int seq0;    // index of that sequence's first tile
@@ -292,6 +297,8 @@ struct WorkSplit {
 
 struct SplitShared {
     int wsum[kWaves];
+    int umin[kWaves];  // per wave: least and greatest tiles per work item (U_b)
+    int umax[kWaves];
     int b;
     int seq0;
     int last[2];
@@ -302,20 +309,53 @@ __device__ __forceinline__ int item_tiles(const DecodeParams& p, int b) {
     return max(1, min((ctx + kTile - 1) / kTile, (int)p.max_tiles));
 }
 
-// first tile of workgroup g
+// First tile of workgroup g.  The balanced split gives workgroup g the tiles
+// [C(g) T / W, C(g+1) T / W) with C the cumulative share: equal shares, or, with a grid
+// of two workgroups per CU (`half` set), wa/1000 of each pair's tiles to the first-half
+// workgroup and the rest to the second-half one.  Workgroups g and g + G/2 share a CU,
+// g dispatched first; the CU's wave arbiter favours the older waves, so with equal
+// shares the first-half workgroup finishes well before its partner.
 __device__ __forceinline__ int split_lo(const DecodeParams& p, const WorkSplit& w, int g) {
-    return w.groups ? (int)((long long)g * w.total / w.groups) : g * (int)p.chunk_tiles;
+    if (!w.groups) return g * (int)p.chunk_tiles;
+    if (!w.half) return (int)((long long)g * w.total / w.groups);
+    const long long c = (long long)w.wa * min(g, w.half) + (long long)(1000 - w.wa) * max(0, g - w.half);
+    return (int)(c * w.total / (1000LL * w.half));
+}
+
+// The workgroup whose range holds tile t (the inverse of split_lo).
+__device__ __forceinline__ int split_group_of(const DecodeParams& p, const WorkSplit& w, int t) {
+    if (!w.groups) return t / (int)p.chunk_tiles;
+    if (!w.half) return (int)(((long long)(t + 1) * w.groups - 1) / w.total);
+    // largest g with split_lo(g) <= t: first half while C(g) T < (t + 1) W
+    const long long n = (long long)(t + 1) * 1000LL * w.half;
+    const long long a = (long long)w.wa * w.total;
+    const long long g = (n - 1) / a;
+    if (g < w.half) return (int)g;
+    return w.half + (int)((n - a * w.half - 1) / ((long long)(1000 - w.wa) * w.total));
 }
 
 // this workgroup's tiles [lo, hi) once T is known
 __device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r) {
     const int g = blockIdx.x;
+    r.half = 0;
+    r.wa = 500;
     if (p.chunk_tiles) {
         r.groups = 0;
         r.lo = (int)min((long long)g * p.chunk_tiles, (long long)r.total);
         r.hi = (int)min((long long)r.lo + p.chunk_tiles, (long long)r.total);
     } else {
         r.groups = min((int)gridDim.x, r.total);
+        // Unequal shares for ragged batches with at least 64 tiles per workgroup (measured:
+        // C4 206 -> 190 us at 700; equal contexts lose, their ranges stop coinciding with
+        // whole work items), and only where every second-half share is at least one tile:
+        // an empty range inside a work item's span of workgroups would never count its
+        // arrival.
+        if (p.split_old_permille != 500 && r.ragged && r.groups == (int)gridDim.x && (gridDim.x & 1) == 0 &&
+            (long long)r.total >= 64LL * gridDim.x &&
+            (long long)(1000 - (int)p.split_old_permille) * r.total >= 500LL * gridDim.x) {
+            r.half = (int)gridDim.x / 2;
+            r.wa = (int)p.split_old_permille;
+        }
         r.lo = g < r.groups ? split_lo(p, r, g) : r.total;
         r.hi = g < r.groups ? split_lo(p, r, g + 1) : r.total;
     }
@@ -338,15 +378,30 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
             const int y = __shfl_up(x, o);
             if (lane >= o) x += y;
         }
+        int umin = b < nb ? u : 0x7fffffff, umax = u;
+#pragma unroll
+        for (int o = 32; o; o >>= 1) {
+            umin = min(umin, __shfl_xor(umin, o));
+            umax = max(umax, __shfl_xor(umax, o));
+        }
         if (lane == 63) sh.wsum[wave] = x;
+        if (lane == 0) {
+            sh.umin[wave] = umin;
+            sh.umax[wave] = umax;
+        }
         __syncthreads();
         int before = 0, all = 0;
+        umin = 0x7fffffff;
+        umax = 0;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             before += w < wave ? sh.wsum[w] : 0;
             all += sh.wsum[w];
+            umin = min(umin, sh.umin[w]);
+            umax = max(umax, sh.umax[w]);
         }
         r.total = __builtin_amdgcn_readfirstlane(all) * ips;
+        r.ragged = __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0);
         split_range(p, r);
         r.b = 0;
         r.seq0 = 0;
@@ -361,16 +416,36 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         r.seq0 = __builtin_amdgcn_readfirstlane(sh.seq0);
         return r;
     }
-    int s = 0;
-    for (int b = threadIdx.x; b < nb; b += kWaves * 64) s += item_tiles(p, b);
+    int s = 0, umin = 0x7fffffff, umax = 0;
+    for (int b = threadIdx.x; b < nb; b += kWaves * 64) {
+        const int u = item_tiles(p, b);
+        s += u;
+        umin = min(umin, u);
+        umax = max(umax, u);
+    }
 #pragma unroll
-    for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
-    if (lane == 0) sh.wsum[wave] = s;
+    for (int o = 32; o; o >>= 1) {
+        s += __shfl_xor(s, o);
+        umin = min(umin, __shfl_xor(umin, o));
+        umax = max(umax, __shfl_xor(umax, o));
+    }
+    if (lane == 0) {
+        sh.wsum[wave] = s;
+        sh.umin[wave] = umin;
+        sh.umax[wave] = umax;
+    }
     __syncthreads();
     int units = 0;
+    umin = 0x7fffffff;
+    umax = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) units += sh.wsum[w];
+    for (int w = 0; w < kWaves; ++w) {
+        units += sh.wsum[w];
+        umin = min(umin, sh.umin[w]);
+        umax = max(umax, sh.umax[w]);
+    }
     r.total = __builtin_amdgcn_readfirstlane(units) * ips;
+    r.ragged = __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0);
     split_range(p, r);
     r.b = 0;
     r.seq0 = 0;
@@ -496,10 +571,8 @@ __device__ __forceinline__ void merge_group(const DecodeParams& p, const WorkSpl
     constexpr int NT = kWaves * 64;
     constexpr int K = (GW * D + NT - 1) / NT;  // outputs per thread: idx = tid + NT * k
     constexpr int NBATCH = 8;
-    const int g0 = w.groups ? (int)(((long long)(c.item0 + 1) * w.groups - 1) / w.total)
-                            : c.item0 / (int)p.chunk_tiles;
-    const int g1 = w.groups ? (int)(((long long)(c.item0 + c.U) * w.groups - 1) / w.total)
-                            : (c.item0 + c.U - 1) / (int)p.chunk_tiles;
+    const int g0 = split_group_of(p, w, c.item0);
+    const int g1 = split_group_of(p, w, c.item0 + c.U - 1);
     const int first_inside = split_lo(p, w, g0) < c.item0 ? 1 : 0;
     // running merge per output in log2 units; -1e30 (not -inf) keeps exp2 finite
     float M[K], A[K], Ls[K];
@@ -575,10 +648,8 @@ __device__ __forceinline__ void arrive_partials(const DecodeParams& p, const Wor
         int last_in = 0;
         if (has) {
             // the workgroups whose ranges meet the item's tiles [item0, item0 + U)
-            const int g0 = w.groups ? (int)(((long long)(item0 + 1) * w.groups - 1) / w.total)
-                                    : item0 / (int)p.chunk_tiles;
-            const int g1 = w.groups ? (int)(((long long)(item0 + U) * w.groups - 1) / w.total)
-                                    : (item0 + U - 1) / (int)p.chunk_tiles;
+            const int g0 = split_group_of(p, w, item0);
+            const int g1 = split_group_of(p, w, item0 + U - 1);
             const uint32_t item = (uint32_t)(b * ips + y);
             const uint32_t seen = atomicAdd(p.arrivals + item, 1u);
             last_in = seen == (uint32_t)(g1 - g0);
@@ -635,10 +706,8 @@ __device__ __forceinline__ void finish_segment(const DecodeParams& p, const floa
     }
     if (whole) return;
     // the workgroups whose ranges meet [item0, item0 + U)
-    const int g0 = w.groups ? (int)(((long long)(item0 + 1) * w.groups - 1) / w.total)
-                            : item0 / (int)p.chunk_tiles;
-    const int g1 = w.groups ? (int)(((long long)(item0 + U) * w.groups - 1) / w.total)
-                            : (item0 + U - 1) / (int)p.chunk_tiles;
+    const int g0 = split_group_of(p, w, item0);
+    const int g1 = split_group_of(p, w, item0 + U - 1);
     // this wave's partial stores have completed (they write through to the device's
     // coherence point, so no L2 write-back is needed) before the arrival is counted
     __builtin_amdgcn_s_waitcnt(0);

@@ -791,6 +791,8 @@ uint32_t* arrival_counters(size_t count, hipStream_t stream) {
     return slot->ptr;
 }
 
+constexpr uint32_t kDefaultOldPermille = 700;
+
 // workgroups per CU of the balanced MFMA split (VSPEC_ROCM_DECODE_WGS_PER_CU, 1..8)
 uint32_t decode_wgs_per_cu() {
     static const uint32_t v = [] {
@@ -799,6 +801,14 @@ uint32_t decode_wgs_per_cu() {
         return x >= 1 && x <= 8 ? (uint32_t)x : 2u;
     }();
     return v;
+}
+
+// Share of the first-half workgroup of each pair sharing a CU under the balanced split,
+// in 1/1000 (VSPEC_ROCM_DECODE_OLD_PERMILLE, 500..900).  Read on every call.
+uint32_t decode_old_permille() {
+    const char* e = getenv("VSPEC_ROCM_DECODE_OLD_PERMILLE");
+    const long x = e ? strtol(e, nullptr, 10) : 0;
+    return x >= 500 && x <= 900 ? (uint32_t)x : kDefaultOldPermille;
 }
 
 struct DecodePlan {
@@ -1326,6 +1336,11 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.k_new = nullptr;
     p.v_new = nullptr;
     p.append_src = src_dtype;
+    // uneven shares for the f16 kernel only (the int4 kernel is bound by its vector ALU
+    // work, which the two workgroups of a CU share either way; measured slower)
+    const bool paired = pl.split && !pl.chunk_tiles && pl.grid_x == 2u * (uint32_t)num_cus() &&
+                        desc->kv.dtype == VSPEC_KV_F16;
+    p.split_old_permille = paired ? decode_old_permille() : 500u;
 
     hipStream_t s = (hipStream_t)desc->stream;
     if (k_new) {
