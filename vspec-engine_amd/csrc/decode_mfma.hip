@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const int n = lane & 15;   // column / token within the tile
 
     const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
-    const WorkSplit ws = work_split(p, ips, split_sh);
+    const WorkSplit ws = work_split<true>(p, ips, split_sh);
     if (ws.lo >= ws.hi) return;
     const ItemCursor first = cursor_at(p, ws);
     if (p.k_new) fused_append<VSPEC_KV_F16, D>(p, ws, first, ips);

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
     const int n = lane & 15;
 
     const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
-    const WorkSplit ws = work_split(p, ips, split_sh);
+    const WorkSplit ws = work_split<false>(p, ips, split_sh);
     if (p.k_new && ws.lo < ws.hi) fused_append<VSPEC_KV_INT4, D>(p, ws, cursor_at(p, ws), ips);
     int b = ws.b;
     int seq0 = ws.seq0;

@@ -315,17 +315,21 @@ __device__ __forceinline__ int item_tiles(const DecodeParams& p, int b) {
 // workgroup and the rest to the second-half one.  Workgroups g and g + G/2 share a CU,
 // g dispatched first; the CU's wave arbiter favours the older waves, so with equal
 // shares the first-half workgroup finishes well before its partner.
+// UNEVEN: the kernel supports unequal pair shares (the f16 kernel); without it the
+// weighted arithmetic is compiled out.
+template <bool UNEVEN>
 __device__ __forceinline__ int split_lo(const DecodeParams& p, const WorkSplit& w, int g) {
     if (!w.groups) return g * (int)p.chunk_tiles;
-    if (!w.half) return (int)((long long)g * w.total / w.groups);
+    if (!UNEVEN || !w.half) return (int)((long long)g * w.total / w.groups);
     const long long c = (long long)w.wa * min(g, w.half) + (long long)(1000 - w.wa) * max(0, g - w.half);
     return (int)(c * w.total / (1000LL * w.half));
 }
 
 // The workgroup whose range holds tile t (the inverse of split_lo).
+template <bool UNEVEN>
 __device__ __forceinline__ int split_group_of(const DecodeParams& p, const WorkSplit& w, int t) {
     if (!w.groups) return t / (int)p.chunk_tiles;
-    if (!w.half) return (int)(((long long)(t + 1) * w.groups - 1) / w.total);
+    if (!UNEVEN || !w.half) return (int)(((long long)(t + 1) * w.groups - 1) / w.total);
     // largest g with split_lo(g) <= t: first half while C(g) T < (t + 1) W
     const long long n = (long long)(t + 1) * 1000LL * w.half;
     const long long a = (long long)w.wa * w.total;
@@ -335,6 +339,7 @@ __device__ __forceinline__ int split_group_of(const DecodeParams& p, const WorkS
 }
 
 // this workgroup's tiles [lo, hi) once T is known
+template <bool UNEVEN>
 __device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r) {
     const int g = blockIdx.x;
     r.half = 0;
@@ -350,19 +355,20 @@ __device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r)
         // whole work items), and only where every second-half share is at least one tile:
         // an empty range inside a work item's span of workgroups would never count its
         // arrival.
-        if (p.split_old_permille != 500 && r.ragged && r.groups == (int)gridDim.x && (gridDim.x & 1) == 0 &&
+        if (UNEVEN && p.split_old_permille != 500 && r.ragged && r.groups == (int)gridDim.x && (gridDim.x & 1) == 0 &&
             (long long)r.total >= 64LL * gridDim.x &&
             (long long)(1000 - (int)p.split_old_permille) * r.total >= 500LL * gridDim.x) {
             r.half = (int)gridDim.x / 2;
             r.wa = (int)p.split_old_permille;
         }
-        r.lo = g < r.groups ? split_lo(p, r, g) : r.total;
-        r.hi = g < r.groups ? split_lo(p, r, g + 1) : r.total;
+        r.lo = g < r.groups ? split_lo<UNEVEN>(p, r, g) : r.total;
+        r.hi = g < r.groups ? split_lo<UNEVEN>(p, r, g + 1) : r.total;
     }
 }
 
 // Block-wide (every thread calls it; the result is uniform).  The host keeps
 // T = hkv * gsplit * sum U_b below 2^31.
+template <bool UNEVEN>
 __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, SplitShared& sh) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -379,16 +385,18 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
             if (lane >= o) x += y;
         }
         int umin = b < nb ? u : 0x7fffffff, umax = u;
+        if constexpr (UNEVEN) {
 #pragma unroll
-        for (int o = 32; o; o >>= 1) {
-            umin = min(umin, __shfl_xor(umin, o));
-            umax = max(umax, __shfl_xor(umax, o));
+            for (int o = 32; o; o >>= 1) {
+                umin = min(umin, __shfl_xor(umin, o));
+                umax = max(umax, __shfl_xor(umax, o));
+            }
+            if (lane == 0) {
+                sh.umin[wave] = umin;
+                sh.umax[wave] = umax;
+            }
         }
         if (lane == 63) sh.wsum[wave] = x;
-        if (lane == 0) {
-            sh.umin[wave] = umin;
-            sh.umax[wave] = umax;
-        }
         __syncthreads();
         int before = 0, all = 0;
         umin = 0x7fffffff;
@@ -397,12 +405,14 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         for (int w = 0; w < kWaves; ++w) {
             before += w < wave ? sh.wsum[w] : 0;
             all += sh.wsum[w];
-            umin = min(umin, sh.umin[w]);
-            umax = max(umax, sh.umax[w]);
+            if constexpr (UNEVEN) {
+                umin = min(umin, sh.umin[w]);
+                umax = max(umax, sh.umax[w]);
+            }
         }
         r.total = __builtin_amdgcn_readfirstlane(all) * ips;
-        r.ragged = __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0);
-        split_range(p, r);
+        r.ragged = UNEVEN ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
+        split_range<UNEVEN>(p, r);
         r.b = 0;
         r.seq0 = 0;
         if (r.lo >= r.hi) return r;
@@ -420,14 +430,18 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
     for (int b = threadIdx.x; b < nb; b += kWaves * 64) {
         const int u = item_tiles(p, b);
         s += u;
-        umin = min(umin, u);
-        umax = max(umax, u);
+        if constexpr (UNEVEN) {
+            umin = min(umin, u);
+            umax = max(umax, u);
+        }
     }
 #pragma unroll
     for (int o = 32; o; o >>= 1) {
         s += __shfl_xor(s, o);
-        umin = min(umin, __shfl_xor(umin, o));
-        umax = max(umax, __shfl_xor(umax, o));
+        if constexpr (UNEVEN) {
+            umin = min(umin, __shfl_xor(umin, o));
+            umax = max(umax, __shfl_xor(umax, o));
+        }
     }
     if (lane == 0) {
         sh.wsum[wave] = s;
@@ -445,8 +459,8 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         umax = max(umax, sh.umax[w]);
     }
     r.total = __builtin_amdgcn_readfirstlane(units) * ips;
-    r.ragged = __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0);
-    split_range(p, r);
+    r.ragged = UNEVEN ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
+    split_range<UNEVEN>(p, r);
     r.b = 0;
     r.seq0 = 0;
     if (r.lo >= r.hi) return r;
@@ -565,15 +579,15 @@ __device__ __forceinline__ void merge_segment(const DecodeParams& p, const float
 // Block-wide, last arrival at work item c: merge the partials of the workgroups g0..g1
 // whose ranges meet its tiles, NBATCH workgroups per batch with all of a batch's loads
 // in flight together (a chain of one load at a time would cost a memory latency each).
-template <int D, int GW>
+template <int D, int GW, bool UNEVEN>
 __device__ __forceinline__ void merge_group(const DecodeParams& p, const WorkSplit& w, const ItemCursor& c,
                                             int tid) {
     constexpr int NT = kWaves * 64;
     constexpr int K = (GW * D + NT - 1) / NT;  // outputs per thread: idx = tid + NT * k
     constexpr int NBATCH = 8;
-    const int g0 = split_group_of(p, w, c.item0);
-    const int g1 = split_group_of(p, w, c.item0 + c.U - 1);
-    const int first_inside = split_lo(p, w, g0) < c.item0 ? 1 : 0;
+    const int g0 = split_group_of<UNEVEN>(p, w, c.item0);
+    const int g1 = split_group_of<UNEVEN>(p, w, c.item0 + c.U - 1);
+    const int first_inside = split_lo<UNEVEN>(p, w, g0) < c.item0 ? 1 : 0;
     // running merge per output in log2 units; -1e30 (not -inf) keeps exp2 finite
     float M[K], A[K], Ls[K];
 #pragma unroll
@@ -648,8 +662,8 @@ __device__ __forceinline__ void arrive_partials(const DecodeParams& p, const Wor
         int last_in = 0;
         if (has) {
             // the workgroups whose ranges meet the item's tiles [item0, item0 + U)
-            const int g0 = split_group_of(p, w, item0);
-            const int g1 = split_group_of(p, w, item0 + U - 1);
+            const int g0 = split_group_of<true>(p, w, item0);
+            const int g1 = split_group_of<true>(p, w, item0 + U - 1);
             const uint32_t item = (uint32_t)(b * ips + y);
             const uint32_t seen = atomicAdd(p.arrivals + item, 1u);
             last_in = seen == (uint32_t)(g1 - g0);
@@ -660,8 +674,8 @@ __device__ __forceinline__ void arrive_partials(const DecodeParams& p, const Wor
     __syncthreads();
     const int merge0 = sh.last[0];
     const int merge1 = sh.last[1];
-    if (merge0) merge_group<D, GW>(p, w, first, tid);
-    if (merge1) merge_group<D, GW>(p, w, last, tid);
+    if (merge0) merge_group<D, GW, true>(p, w, first, tid);
+    if (merge1) merge_group<D, GW, true>(p, w, last, tid);
 }
 
 // Merge the kWaves per-wave states of one segment (tiles [tile_begin, tile_end) of the
@@ -706,8 +720,8 @@ __device__ __forceinline__ void finish_segment(const DecodeParams& p, const floa
     }
     if (whole) return;
     // the workgroups whose ranges meet [item0, item0 + U)
-    const int g0 = split_group_of(p, w, item0);
-    const int g1 = split_group_of(p, w, item0 + U - 1);
+    const int g0 = split_group_of<false>(p, w, item0);
+    const int g1 = split_group_of<false>(p, w, item0 + U - 1);
     // this wave's partial stores have completed (they write through to the device's
     // coherence point, so no L2 write-back is needed) before the arrival is counted
     __builtin_amdgcn_s_waitcnt(0);
@@ -726,7 +740,7 @@ __device__ __forceinline__ void finish_segment(const DecodeParams& p, const floa
     c.U = U;
     c.item0 = item0;
     c.seq0 = 0;
-    merge_group<D, GW>(p, w, c, tid);
+    merge_group<D, GW, false>(p, w, c, tid);
 }
 
 }  // namespace vkv
