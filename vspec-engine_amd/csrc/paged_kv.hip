@@ -793,12 +793,13 @@ uint32_t* arrival_counters(size_t count, hipStream_t stream) {
 
 constexpr uint32_t kDefaultOldPermille = 700;
 
-// workgroups per CU of the balanced MFMA split (VSPEC_ROCM_DECODE_WGS_PER_CU, 1..8)
-uint32_t decode_wgs_per_cu() {
+// workgroups per CU of the balanced MFMA split: VSPEC_ROCM_DECODE_WGS_PER_CU (1..8) when
+// set, else 0 (the plan decides)
+uint32_t decode_wgs_per_cu_env() {
     static const uint32_t v = [] {
         const char* e = getenv("VSPEC_ROCM_DECODE_WGS_PER_CU");
         const long x = e ? strtol(e, nullptr, 10) : 0;
-        return x >= 1 && x <= 8 ? (uint32_t)x : 2u;
+        return x >= 1 && x <= 8 ? (uint32_t)x : 0u;
     }();
     return v;
 }
@@ -860,7 +861,12 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
             grid = (bound + pl->chunk_tiles - 1) / pl->chunk_tiles;
         } else {
             pl->chunk_tiles = 0;
-            grid = (uint64_t)decode_wgs_per_cu() * (uint64_t)num_cus();
+            // two workgroups per CU; small f16 batches (under 64 tiles per workgroup at two
+            // per CU) take one, which halves the cross-workgroup merges per work item
+            // (C2: 41.6 -> 38.9 us; the int4 kernel, bound by vector ALU work, needs both)
+            uint32_t wpc = decode_wgs_per_cu_env();
+            if (!wpc) wpc = d->kv.dtype == VSPEC_KV_F16 && bound < 128ull * (uint64_t)num_cus() ? 1u : 2u;
+            grid = (uint64_t)wpc * (uint64_t)num_cus();
             if (grid > bound) grid = bound;
         }
         pl->grid_x = (uint32_t)(grid ? grid : 1);
