@@ -117,7 +117,8 @@ typedef struct VspecPagedAttnDesc {
     const int32_t* block_tables;     /* device [batch][max_blocks_per_seq] */
     uint32_t max_blocks_per_seq;
     const int32_t* ctx_lens;         /* device [batch] */
-    uint32_t max_ctx_len;            /* host upper bound of ctx_lens (sizes the workspace) */
+    uint32_t max_ctx_len;            /* host upper bound of ctx_lens (sizes the workspace);
+                                        0: max_blocks_per_seq * block_tokens */
     const float* q;                  /* device [batch][Hq][D] f32 */
     float* out;                      /* device [batch][Hq][D] f32 (ctx 0 -> zeros) */
     float scale;                     /* <= 0: 1/sqrtf(D) */

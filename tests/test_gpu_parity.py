@@ -330,6 +330,29 @@ def test_decode_uneven_pair_shares(oracle, gpu):
     check_attention(oracle, case, outs[700], 1, subset=[0, 5, 11, 19])
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+def test_decode_max_ctx_len_zero(oracle, gpu, dtype):
+    """max_ctx_len 0 stands for the block table's capacity: the same attention as with the
+    true bound (the f16 / int4 split does not depend on it; the f32 partitions do, which
+    moves rounding only)."""
+    import torch
+    import vspec_rocm as vr
+
+    say(f"[max_ctx_len 0] dtype={dtype}")
+    case = make_case(oracle, dtype, 3, 8, 2, 128, 16, [300, 75, 1000], seed=61, num_blocks=96)
+    pool = build_both(oracle, case, gpu)
+    tab = torch.from_numpy(np.pad(case.tables, ((0, 0), (0, 4)), constant_values=-1)).to(gpu)
+    cl = torch.from_numpy(case.ctx).to(gpu)
+    q = torch.from_numpy(case.q).to(gpu)
+    a = vr.paged_decode(pool, tab, cl, q, max_ctx_len=0, numerics=1).cpu().numpy()
+    b = vr.paged_decode(pool, tab, cl, q, max_ctx_len=case.tmax, numerics=1).cpu().numpy()
+    if dtype == DTYPE_F32:
+        assert np.abs(a - b).max() < 1e-5
+    else:
+        assert np.array_equal(a, b)
+    check_attention(oracle, case, a, 1)
+
+
 def test_decode_partition_invariance(oracle, gpu):
     """Split-K partition size changes rounding only."""
     say("[partitions]")

@@ -842,7 +842,14 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
         set_err("paged_decode: GQA group %u unsupported (need <= 4 or a multiple of 4)", g);
         return 0;
     }
-    const uint32_t max_tiles = (d->max_ctx_len + kTile - 1) / kTile;
+    // the host's bound on ctx_lens; 0 stands for the block table's capacity
+    const uint64_t ctx_bound = d->max_ctx_len ? (uint64_t)d->max_ctx_len
+                                              : (uint64_t)d->max_blocks_per_seq * d->kv.block_tokens;
+    if (ctx_bound > (uint64_t)INT32_MAX) {
+        set_err("paged_decode: context bound beyond 2^31 tokens");
+        return 0;
+    }
+    const uint32_t max_tiles = (uint32_t)((ctx_bound + kTile - 1) / kTile);
     pl->split = d->kv.dtype != VSPEC_KV_F32;
     if (pl->split) {
         // every workgroup streams an equal share of all work items' tiles
