@@ -478,6 +478,61 @@ def test_decode_step_fused_append(oracle, gpu, dtype, Hq, Hkv, D, P, pt, src16):
     check_attention(oracle, full, got.cpu().numpy(), 1)
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
+def test_decode_step_in_hip_graph(oracle, gpu, dtype):
+    """A decode step (fused append + attention) captured into a HIP graph after one eager
+    call on the capture stream (which sets up that stream's merge counters and the
+    workspace): every replay, with eager decodes of another batch and synchronisations in
+    between, equals the eager step bit for bit, and the pool bytes stay those of the eager
+    append (every launch returns the counters to zero; no memset is recorded)."""
+    import torch
+    import vspec_rocm as vr
+
+    say(f"[hip graph] dtype={dtype}")
+    ctx = np.array([700, 33, 1501, 2049, 9], np.int32)
+    case = make_case(oracle, dtype, len(ctx), 32, 8, 128, 16, ctx, seed=81)
+    other = make_case(oracle, DTYPE_F16, 3, 8, 2, 64, 16, [100, 57, 300], seed=82)
+    pool = build_both(oracle, case, gpu)
+    pool_o = build_both(oracle, other, gpu)
+    tab = torch.from_numpy(case.tables).to(gpu)
+    cl = torch.from_numpy(case.ctx).to(gpu)
+    q = torch.from_numpy(case.q).to(gpu)
+    B = len(ctx)
+    last = np.maximum(ctx - 1, 0)
+    kd = _np_to_dev(np.ascontiguousarray(case.k_tokens[np.arange(B), last]), gpu)
+    vd = _np_to_dev(np.ascontiguousarray(case.v_tokens[np.arange(B), last]), gpu)
+    ws = torch.empty(1 << 22, dtype=torch.uint8, device=gpu)
+    out = torch.full_like(q, float("nan"))
+    s = torch.cuda.Stream()
+
+    def step():
+        vr.paged_decode_step(pool, tab, cl, q, kd, vd, max_ctx_len=case.tmax, numerics=1, out=out,
+                             workspace=ws, stream=s.cuda_stream)
+
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()  # eager: counters and workspace exist before capture
+    torch.cuda.synchronize()
+    want = out.clone()
+    want_pool = [None if a is None else a.copy() for a in pool_bytes(pool)]
+    check_attention(oracle, case, want.cpu().numpy(), 1)
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    for rep in range(4):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep}"
+        for a, b in zip(pool_bytes(pool), want_pool):
+            if b is not None:
+                assert np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+        # eager work between replays, on the default stream
+        run_decode(other, pool_o, gpu, 1)
+
+
 def test_decode_step_rejects_bad_source(gpu):
     import torch
     import vspec_rocm as vr
