@@ -244,6 +244,28 @@ def test_decode_edges(oracle, gpu, dtype, D, Hq, Hkv):
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+@pytest.mark.parametrize("P", [48, 64])
+def test_decode_block_sizes(oracle, gpu, dtype, P):
+    """Blocks of 48 and 64 tokens (the kernels' generic block size: several 16-token tiles
+    per block) with contexts around block and tile edges: bit-exact pools, attention within
+    tolerance in both modes and with fixed-size partitions."""
+    import torch
+    import vspec_rocm as vr
+
+    ctx = [1, P - 1, P, P + 1, 3 * P + 17, 200, 0]
+    say(f"[block sizes] dtype={dtype} P={P}")
+    case = make_case(oracle, dtype, len(ctx), 16, 4, 128, P, ctx, seed=3 * P + dtype, num_blocks=24)
+    pool = build_both(oracle, case, gpu)
+    assert_pools_equal(case.host, pool)
+    for mode in (0, 1):
+        got = run_decode(case, pool, gpu, mode)
+        assert np.all(got[-1] == 0.0)
+        check_attention(oracle, case, got, mode, subset=range(len(ctx) - 1))
+    got = run_decode(case, pool, gpu, 1, partition_tokens=32)
+    check_attention(oracle, case, got, 1, subset=range(len(ctx) - 1))
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
 def test_decode_outliers_fire_clamp(oracle, gpu, dtype):
     """Large outliers make the std-clamp (and in mode R the +-16 clip and +-24 logit
     clip) change the result; the GPU must follow the reference there too (the f16 and
