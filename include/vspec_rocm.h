@@ -59,6 +59,9 @@ typedef struct VspecPagedKV {
     void* v_data;           /* device */
     uint16_t* k_scales;     /* device, int4 only */
     uint16_t* v_scales;     /* device, int4 only */
+    uint32_t* k_flags;      /* device, int4 only, or NULL: per 16-token tile of a (block, kv
+                               head) one word, bit t set when key t may reach the std clamp
+                               (written on append; with NULL the decode screens every key) */
 } VspecPagedKV;
 
 /* ---- pools: hipMalloc-backed, replaces the host malloc of capi.c:2188-2219 ---- */

@@ -47,7 +47,8 @@ def test_pool_bytes_formula():
     rows = 10 * 8 * 16
     assert L.vspec_rocm_kv_pool_bytes(1, 10, 16, 8, 128) == 2 * rows * 256
     assert L.vspec_rocm_kv_pool_bytes(0, 10, 16, 8, 64) == 2 * rows * 256
-    assert L.vspec_rocm_kv_pool_bytes(2, 10, 16, 8, 128) == 2 * rows * (64 + 8)
+    # int4: codes + scales, and one clamp-flag word per 16-token tile of K
+    assert L.vspec_rocm_kv_pool_bytes(2, 10, 16, 8, 128) == 2 * rows * (64 + 8) + (rows // 16) * 4
 
 
 def test_argument_validation_without_gpu():

@@ -34,6 +34,27 @@ def gpu():
     return torch.device("cuda:0")
 
 
+@pytest.fixture(params=["plan", "always"])
+def flag_gate(request):
+    """int4 decode: "plan" lets the host pick the clamp-flag kernel (shares of >= 64 tiles
+    per workgroup) or the screen-every-tile one; "always" forces the flag kernel
+    (VSPEC_ROCM_DECODE_FLAG_MIN_TILES=0, read on every call).  Cases of other pool
+    dtypes run once."""
+    import os
+
+    dtype = request.node.callspec.params.get("dtype", DTYPE_INT4)
+    if request.param == "always" and dtype != DTYPE_INT4:
+        pytest.skip("clamp flags exist for int4 pools only")
+    old = os.environ.get("VSPEC_ROCM_DECODE_FLAG_MIN_TILES")
+    if request.param == "always":
+        os.environ["VSPEC_ROCM_DECODE_FLAG_MIN_TILES"] = "0"
+    yield request.param
+    if old is None:
+        os.environ.pop("VSPEC_ROCM_DECODE_FLAG_MIN_TILES", None)
+    else:
+        os.environ["VSPEC_ROCM_DECODE_FLAG_MIN_TILES"] = old
+
+
 def _np_to_dev(a, dev):
     import torch
 
@@ -227,7 +248,7 @@ def test_compact_bitexact(oracle, gpu):
 # ----------------------------------------------------------------------------- decode edge cases
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
 @pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 8), (128, 8, 4), (128, 16, 4), (128, 16, 2), (64, 6, 2)])
-def test_decode_edges(oracle, gpu, dtype, D, Hq, Hkv):
+def test_decode_edges(oracle, gpu, flag_gate, dtype, D, Hq, Hkv):
     """Ragged contexts around tile/block edges, GQA groups 1/2/3/4/8, garbage (NaN)
     beyond each context, several partition sizes."""
     ctx = [1, 15, 16, 17, 33, 64, 100, 0]
@@ -245,7 +266,7 @@ def test_decode_edges(oracle, gpu, dtype, D, Hq, Hkv):
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
 @pytest.mark.parametrize("P", [48, 64])
-def test_decode_block_sizes(oracle, gpu, dtype, P):
+def test_decode_block_sizes(oracle, gpu, flag_gate, dtype, P):
     """Blocks of 48 and 64 tokens (the kernels' generic block size: several 16-token tiles
     per block) with contexts around block and tile edges: bit-exact pools, attention within
     tolerance in both modes and with fixed-size partitions."""
@@ -266,7 +287,7 @@ def test_decode_block_sizes(oracle, gpu, dtype, P):
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
-def test_decode_outliers_fire_clamp(oracle, gpu, dtype):
+def test_decode_outliers_fire_clamp(oracle, gpu, flag_gate, dtype):
     """Large outliers make the std-clamp (and in mode R the +-16 clip and +-24 logit
     clip) change the result; the GPU must follow the reference there too (the f16 and
     int4 kernels take their exact-score path for these keys)."""
@@ -286,10 +307,58 @@ def test_decode_outliers_fire_clamp(oracle, gpu, dtype):
         check_attention(oracle, case, got, mode)
 
 
+def test_int4_clamp_flags_are_conservative(oracle, gpu):
+    """Every key the append leaves unflagged is one the reference's clamp chain leaves
+    alone: the std clamp (alpha 4.5, attention_ref.c:56) returns it unchanged and no
+    element reaches the 3-bit input clip of 16, so the decode may score it without
+    clamping.  Keys: Gaussian rows, rows with one large element, rows scaled by 20
+    (elements beyond 16), constant rows (std 0) and near-constant rows.  The flags are
+    also not trivially all set: most Gaussian rows stay clear."""
+    import torch
+
+    say("[flags] build")
+    case = make_case(oracle, DTYPE_INT4, 3, 8, 2, 128, 16, [300, 77, 160], seed=93, src16=False)
+    k = case.k_tokens.copy()
+    k[0, ::7, 0, 3] = 40.0
+    k[0, 1::7, 1, 5] = 6.5
+    k[1, ::5, 1, 100] = -25.0
+    k[0, 10, 1, :] *= 20.0
+    k[2, :40] *= 20.0
+    k[2, 40:60] = 0.75
+    k[2, 60:80] = 0.75 + 1e-3 * k[2, 60:80]
+    case.k_tokens = k
+    pool = build_both(oracle, case, gpu)
+    assert_pools_equal(case.host, pool)
+    flags = pool.kf.cpu().numpy().view(np.uint32)
+    keys, _, _, _ = oracle.paged_gather(case.host, case.tables, case.ctx, out_mode=1)
+    H, P = case.Hkv, case.P
+    clear = fired = total = 0
+    off = 0
+    for b in range(case.B):
+        for t in range(int(case.ctx[b])):
+            phys = int(case.tables[b, t // P])
+            for h in range(H):
+                word = (phys * H + h) * (P // 16) + (t % P) // 16
+                on = bool((flags[word] >> (t % 16)) & 1)
+                x = np.ascontiguousarray(keys[off + t, h])
+                y = np.empty_like(x)
+                oracle.lib.vo_dynamic_clamp_std(ptr(x, _f32p), x.size, 4.5, ptr(y, _f32p))
+                moved = not np.array_equal(x, y) or np.abs(x).max() >= 16.0
+                total += 1
+                fired += moved
+                if not on:
+                    clear += 1
+                    assert not moved, f"unflagged key b={b} t={t} h={h} is changed by the clamp"
+        off += int(case.ctx[b])
+    say(f"[flags] keys {total} clamped {fired} unflagged {clear}")
+    assert fired > 0
+    assert clear >= 0.8 * (total - fired)
+
+
 # ----------------------------------------------------------------------------- configs 2-4
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_config2_3_qwen_decode(oracle, gpu, dtype, mode):
+def test_config2_3_qwen_decode(oracle, gpu, flag_gate, dtype, mode):
     """C2 (fp16) and C3 (int4 quantize-on-write): B=16, GQA 32/8, D=128, T=2048+1."""
     say(f"[c2/c3] dtype={dtype} mode={mode} build")
     case = qwen_c2(oracle, dtype)
@@ -353,7 +422,7 @@ def test_decode_uneven_pair_shares(oracle, gpu):
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
-def test_decode_max_ctx_len_zero(oracle, gpu, dtype):
+def test_decode_max_ctx_len_zero(oracle, gpu, flag_gate, dtype):
     """max_ctx_len 0 stands for the block table's capacity: the same attention as with the
     true bound (the f16 / int4 split does not depend on it; the f32 partitions do, which
     moves rounding only)."""
@@ -450,7 +519,7 @@ def test_decode_back_to_back_and_streams(oracle, gpu):
     (DTYPE_F16, 8, 2, 128, 16, 0), (DTYPE_F16, 16, 2, 64, 32, 0), (DTYPE_F16, 32, 8, 128, 16, 32),
     (DTYPE_INT4, 8, 2, 128, 16, 0), (DTYPE_INT4, 16, 2, 64, 32, 32), (DTYPE_F32, 8, 2, 128, 16, 0)])
 @pytest.mark.parametrize("src16", [False, True])
-def test_decode_step_fused_append(oracle, gpu, dtype, Hq, Hkv, D, P, pt, src16):
+def test_decode_step_fused_append(oracle, gpu, flag_gate, dtype, Hq, Hkv, D, P, pt, src16):
     """vspec_rocm_paged_decode_step (append of the decode token at ctx - 1, then attention;
     one launch for f16 / int4 pools) against kv_append + paged_decode on a second pool
     built identically: the same pool bytes and the same outputs bit for bit, both equal to
@@ -501,7 +570,7 @@ def test_decode_step_fused_append(oracle, gpu, dtype, Hq, Hkv, D, P, pt, src16):
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
-def test_decode_step_in_hip_graph(oracle, gpu, dtype):
+def test_decode_step_in_hip_graph(oracle, gpu, flag_gate, dtype):
     """A decode step (fused append + attention) captured into a HIP graph after one eager
     call on the capture stream (which sets up that stream's merge counters and the
     workspace): every replay, with eager decodes of another batch and synchronisations in
@@ -572,7 +641,7 @@ def test_decode_step_rejects_bad_source(gpu):
 
 # ----------------------------------------------------------------------------- config 5
 @pytest.mark.parametrize("mode", [0, 1])
-def test_config5_chunk_evict_compact(oracle, gpu, mode):
+def test_config5_chunk_evict_compact(oracle, gpu, flag_gate, mode):
     """C5 at reduced context: int4 contexts, a 512-token fp16 chunk appended with
     quantize-on-write, oldest 25% of blocks evicted, survivors compacted, decode."""
     import torch

@@ -12,6 +12,7 @@ struct AppendParams {
     uint8_t* v;
     uint16_t* ks;
     uint16_t* vs;
+    uint32_t* kf;  // int4 clamp flags or null
     const int32_t* block_tables;
     const int32_t* start_pos;
     // packed-token mode (token_item != null): source token b (n_new == 1) goes to
@@ -44,9 +45,23 @@ constexpr int append_ept(int dt) { return dt == VSPEC_KV_INT4 ? 32 : 8; }
 // Chunk c of the token-head row of K (which 0) or V (which 1) whose first source element
 // is src_el, written at position pos of block-table row `seq`, kv head h.  Positions past
 // the table, behind an invalid entry or (with rotary tables) past max_pos are not written.
+// A clamp-flag update held back by the caller: flag word `word` gets bit `bit` set or
+// cleared.
+struct FlagOp {
+    uint32_t* word;
+    uint32_t bit;
+    bool set;
+};
+
+__device__ __forceinline__ void apply_flag(const FlagOp& f) {
+    if (!f.word) return;
+    if (f.set) atomicOr(f.word, f.bit);
+    else atomicAnd(f.word, ~f.bit);
+}
+
 template <int DT, int SRC>
 __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq, uint32_t pos, uint32_t h,
-                                             uint32_t c, int which, size_t src_el) {
+                                             uint32_t c, int which, size_t src_el, FlagOp* defer = nullptr) {
     constexpr int EPT = append_ept(DT);
     const uint32_t lb = pos / p.block_tokens;
     if (lb >= p.max_blocks) return;
@@ -151,11 +166,43 @@ __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq
         if ((s16 & 0x7fffu) >= 0x7c00u) s16 = 0x7bffu;
         const float sc = half_bits_to_float(s16);
         uint32_t w[4] = {0u, 0u, 0u, 0u};
+        int c1 = 0, c2 = 0, cm = 0;  // sum, sum of squares and largest magnitude of the codes
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
             const float rr = rintf(x[e] / sc);
             const int code = rr > 7.0f ? 7 : (rr >= -8.0f ? (int)rr : -8);
             w[e / 8] |= ((uint32_t)code & 0xfu) << (4 * (e % 8));
+            c1 += code;
+            c2 += code * code;
+            cm = max(cm, code < 0 ? -code : code);
+        }
+        if (!which && p.kf) {
+            // Clamp flag of the key (attention_ref.c:56 clips every key at its std threshold):
+            // set when some element may reach alpha * std (alpha 4.5, the reference default;
+            // threshold capped at 16 as in 3-bit mode) of the dequantised row.  Mean and
+            // E[x^2] come from the code sums of the row's groups, which sit in lanes 2c of
+            // an aligned run of 2 * head_dim / 32 lanes (the append work items of one row);
+            // the 2^-10 margins cover the one-pass variance (the decode kernel's screen test,
+            // run once per key here).
+            float s1 = sc * (float)c1;
+            float s2 = (sc * sc) * (float)c2;
+            float m = sc * (float)cm;
+            for (uint32_t o = 2; o < 2 * (p.head_dim / 32); o <<= 1) {
+                s1 += __shfl_xor(s1, (int)o);
+                s2 += __shfl_xor(s2, (int)o);
+                m = fmaxf(m, __shfl_xor(m, (int)o));
+            }
+            const float mean = s1 / (float)p.head_dim;
+            const float ex2 = s2 / (float)p.head_dim;
+            const float var1 = ex2 - mean * mean;
+            const float th1 = fminf(fmaxf(1e-6f, 4.5f * sqrtf(fmaxf(var1, 0.f))), 16.0f);
+            const bool flag = m > th1 * (1.0f - 0.0009765625f) || var1 <= ex2 * 0.0009765625f;
+            if (c == 0) {
+                const FlagOp op = {p.kf + ((size_t)phys * p.hkv + h) * (p.block_tokens / 16) + slot / 16,
+                                   1u << (slot % 16), flag};
+                if (defer) *defer = op;
+                else apply_flag(op);
+            }
         }
         const size_t bh = (size_t)phys * p.hkv + h;
         if (which) {
@@ -189,7 +236,8 @@ __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq
 // read the rows written here (they belong to the item's last tile), except the owners of
 // the other q-head groups of the same kv head, which write the same bytes themselves.
 template <int DT, int D>
-__device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCursor c, const int ips) {
+__device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCursor c, const int ips,
+                             FlagOp& pending, uint32_t* pend_lds) {
     constexpr int EPT = append_ept(DT);
     constexpr int kItems = D / EPT * 2;  // append work items per token-head row (K and V)
     static_assert(kItems <= kWaves * 64, "one pass of the workgroup's threads");
@@ -198,6 +246,7 @@ __device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCur
     a.v = const_cast<uint8_t*>(p.v);
     a.ks = const_cast<uint16_t*>(p.ks);
     a.vs = const_cast<uint16_t*>(p.vs);
+    a.kf = const_cast<uint32_t*>(p.kf);
     a.block_tables = p.block_tables;
     a.start_pos = nullptr;
     a.token_item = nullptr;
@@ -217,6 +266,11 @@ __device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCur
     a.max_blocks = p.max_blocks;
     a.num_blocks = p.num_blocks;
     const int t = (int)threadIdx.x;
+    // int4 clamp flags (thread 0 of each row): the first one is handed back to the caller,
+    // which applies it after the barrier below (so the barrier does not wait for it) and,
+    // with pend_lds, is published there as {word index, bit, set} for the tile loop to patch
+    // into the word it loads; any further ones are applied at once
+    pending = {nullptr, 0u, false};
     while (true) {
         const int last = c.item0 + c.U - 1;
         if (last >= ws.lo && last < ws.hi) {
@@ -225,15 +279,25 @@ __device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCur
                 const uint32_t hk = (uint32_t)c.y / p.gsplit;
                 const uint32_t ch = (uint32_t)t >> 1;
                 const size_t src_el = ((size_t)c.b * p.hkv + hk) * D + (size_t)ch * EPT;
+                FlagOp op = {nullptr, 0u, false};
                 if (p.append_src == VSPEC_KV_F32) {
-                    append_chunk<DT, VSPEC_KV_F32>(a, (uint32_t)c.b, (uint32_t)ctx - 1u, hk, ch, t & 1, src_el);
+                    append_chunk<DT, VSPEC_KV_F32>(a, (uint32_t)c.b, (uint32_t)ctx - 1u, hk, ch, t & 1, src_el, &op);
                 } else {
-                    append_chunk<DT, VSPEC_KV_F16>(a, (uint32_t)c.b, (uint32_t)ctx - 1u, hk, ch, t & 1, src_el);
+                    append_chunk<DT, VSPEC_KV_F16>(a, (uint32_t)c.b, (uint32_t)ctx - 1u, hk, ch, t & 1, src_el, &op);
+                }
+                if (op.word) {
+                    if (!pending.word) pending = op;
+                    else apply_flag(op);
                 }
             }
         }
         if (c.item0 + c.U >= ws.hi) break;
         cursor_next(p, ips, c);
+    }
+    if (pend_lds && t == 0) {
+        pend_lds[0] = pending.word ? (uint32_t)(pending.word - p.kf) : 0xffffffffu;
+        pend_lds[1] = pending.bit;
+        pend_lds[2] = pending.set ? pending.bit : 0u;
     }
     __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
     __syncthreads();

@@ -74,7 +74,8 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const WorkSplit ws = work_split<true>(p, ips, split_sh);
     if (ws.lo >= ws.hi) return;
     const ItemCursor first = cursor_at(p, ws);
-    if (p.k_new) fused_append<VSPEC_KV_F16, D>(p, ws, first, ips);
+    FlagOp no_flags;  // f16 pools keep no clamp flags
+    if (p.k_new) fused_append<VSPEC_KV_F16, D>(p, ws, first, ips, no_flags, nullptr);
 
 
     // ---- q' = clip(q) * scale * log2(e) of work item c (segment s) for this wave, and

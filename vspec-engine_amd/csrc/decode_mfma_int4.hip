@@ -59,6 +59,8 @@ struct I4Frags {
     uint32_t ks_own;      // K scale of (token n, this lane's group), low 16 bits
     uint2 ks_col;         // K scales of tokens 4g..4g+3 for column group (n/4) % G
     uint32_t vs[2 * NQ];  // V scales of tokens 4g..4g+3, token-major (G per token)
+    uint32_t flags;       // clamp flags of the tile's 16 keys (the same in every lane)
+    uint32_t fword;       // index of that flag word (wave-uniform)
 };
 
 // fp16 number i of a packed array, as the f16 operand of a mixed-precision FMA
@@ -70,7 +72,9 @@ __device__ __forceinline__ _Float16 half_at(const uint32_t* w, int i) {
 #define VSPEC_I4_MIN_WG_PER_CU 2
 #endif
 
-template <int D, int GW, int PB, int NB>
+// FL: the tile loop takes the pool's clamp flags (and screens only what they cannot say);
+// without FL it screens every tile, a lighter loop for short per-workgroup shares.
+template <int D, int GW, int PB, int NB, bool FL>
 __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(DecodeParams p) {
     constexpr int NQ = D / 32;   // code dwords per lane = QK MFMAs per tile = groups
     constexpr int NG = D / 32;
@@ -89,7 +93,21 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 
     const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
     const WorkSplit ws = work_split<false>(p, ips, split_sh);
-    if (p.k_new && ws.lo < ws.hi) fused_append<VSPEC_KV_INT4, D>(p, ws, cursor_at(p, ws), ips);
+    FlagOp pending = {nullptr, 0u, false};
+    __shared__ uint32_t pend_lds[3];  // the fused append's first clamp flag: {word, bit, value}
+    if (FL && threadIdx.x == 0) pend_lds[0] = 0xffffffffu;
+    if (p.k_new && ws.lo < ws.hi)
+        fused_append<VSPEC_KV_INT4, D>(p, ws, cursor_at(p, ws), ips, pending, FL ? pend_lds : nullptr);
+    uint32_t pend_word = 0xffffffffu, pend_bit = 0u, pend_val = 0u;
+    if (FL) {
+        __syncthreads();
+        pend_word = __builtin_amdgcn_readfirstlane(pend_lds[0]);
+        pend_bit = __builtin_amdgcn_readfirstlane(pend_lds[1]);
+        pend_val = __builtin_amdgcn_readfirstlane(pend_lds[2]);
+    }
+    // the append's first flag update, after the barrier: it overlaps the first tile loads
+    // instead of holding up the barrier (a tile read of its word takes the patched value)
+    apply_flag(pending);
     int b = ws.b;
     int seq0 = ws.seq0;
     for (int pos = ws.lo; pos < ws.hi;) {
@@ -161,6 +179,12 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         const int own_group = (g * NQ) >> 2;
         const int col_group = (n >> 2) % NG;
 
+        // clamp flags from the pool (see screen below); `fused`: this launch appended each
+        // work item's last token
+        const bool flags_on = FL && p.alpha >= 4.5f;
+        const bool fused = p.k_new != nullptr;
+        auto valid_mask = [](int nvalid) -> uint32_t { return nvalid >= kTile ? 0xffffu : (1u << nvalid) - 1u; };
+
         // Loads are issued unconditionally (a tile past the range or behind an invalid
         // table entry reads block 0 and reports false): with no branches around them the
         // compiler counts outstanding loads exactly and waits only for the tile it needs.
@@ -188,6 +212,10 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             }
             f.ks_own = load_stream_u16(p.ks + (bh * NG + own_group) * P + slot0 + n);
             f.ks_col = load_stream2(p.ks + (bh * NG + col_group) * P + slot0 + 4 * g);
+            // a vector load, waited for with the tile's other loads (a scalar load would be
+            // waited for by every LDS wait of the loop: the two share a counter)
+            f.fword = (uint32_t)(bh * (P / kTile) + slot0 / kTile);
+            f.flags = flags_on ? __hip_atomic_load(p.kf + f.fword, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) : 0u;
             const uint4* vs = reinterpret_cast<const uint4*>(p.vs + (bh * P + slot0 + 4 * g) * NG);
 #pragma unroll
             for (int i = 0; i < NQ / 2; ++i) {
@@ -212,7 +240,10 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // Clamp screen of key n of a tile (this lane: one group's codes): mean and E[x^2]
         // from integer code sums; this group's |x| <= 8 * scale.  `flag` is set in a lane
         // whose group may reach the clamp threshold; key n is flagged when any of its four
-        // lanes is (tokens() folds the wave's ballot).
+        // lanes is (tokens() folds the wave's ballot).  Pools with clamp flags skip it: the
+        // append ran the same test once per key (alpha 4.5; a larger alpha only clamps
+        // less), except in the tile that this launch's fused append wrote into, whose flag
+        // word the scalar cache may hold from before the write.
         struct Screen {
             float mean;
             bool flag;
@@ -263,7 +294,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         };
 
         // Exact fp32 scores for the flagged keys of a tile (reference clamp, two-pass variance).
-        auto exact = [&](const I4Frags<D>& f, const Screen& sn, const uint32_t flagged, f4_t& sc) {
+        auto exact = [&](const I4Frags<D>& f, const uint32_t flagged, f4_t& sc) {
             const float s_own = (float)__builtin_bit_cast(_Float16, (uint16_t)f.ks_own);
             float x[8 * NQ];
 #pragma unroll
@@ -271,9 +302,13 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[8 * m + e] = nibble(f.k[m], e) * s_own;
             }
+            float s1 = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8 * NQ; ++i) s1 += x[i];
+            const float mean = add_rows(s1) * (1.0f / D);
             float v2 = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8 * NQ; ++i) v2 = fmaf(x[i] - sn.mean, x[i] - sn.mean, v2);
+            for (int i = 0; i < 8 * NQ; ++i) v2 = fmaf(x[i] - mean, x[i] - mean, v2);
             v2 = add_rows(v2);
             const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v2 * (1.0f / D))), p.input_clip);
             float part[GW];
@@ -321,16 +356,34 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         auto process = [&](I4Frags<D>& fa, I4Frags<D>& fb, const bool oka, const bool okb, const int tile_a) {
             const int nva = oka ? min(kTile, ctx - tile_a * kTile) : 0;
             const int nvb = okb ? min(kTile, ctx - (tile_a + 1) * kTile) : 0;
-            // both tiles in one basic block: their chains interleave
-            const Screen sna = screen(fa, nva);
-            const Screen snb = screen(fb, nvb);
-            f4_t sa = qk(fa);
-            f4_t sb = qk(fb);
-            const uint32_t fla = tokens(__builtin_amdgcn_ballot_w64(sna.flag));
-            const uint32_t flb = tokens(__builtin_amdgcn_ballot_w64(snb.flag));
+            // clamp flags: from the pool, or from the screen (both tiles in one basic block:
+            // their chains interleave)
+            // the tile this launch appended into: its word with the appended key's flag
+            // patched in, or (another appended item of this range) the screen
+            const bool scr_a = !flags_on || (fused && tile_a == U - 1 && fa.fword != pend_word);
+            const bool scr_b = !flags_on || (fused && tile_a + 1 == U - 1 && fb.fword != pend_word);
+            auto word_of = [&](const I4Frags<D>& f) -> uint32_t {
+                const uint32_t w = __builtin_amdgcn_readfirstlane(f.flags);
+                return f.fword == pend_word ? (w & ~pend_bit) | pend_val : w;
+            };
+            uint32_t fla, flb;
+            f4_t sa, sb;
+            if (scr_a || scr_b) {
+                const Screen sna = screen(fa, nva);
+                const Screen snb = screen(fb, nvb);
+                sa = qk(fa);
+                sb = qk(fb);
+                fla = scr_a ? tokens(__builtin_amdgcn_ballot_w64(sna.flag)) : word_of(fa) & valid_mask(nva);
+                flb = scr_b ? tokens(__builtin_amdgcn_ballot_w64(snb.flag)) : word_of(fb) & valid_mask(nvb);
+            } else {
+                sa = qk(fa);
+                sb = qk(fb);
+                fla = word_of(fa) & valid_mask(nva);
+                flb = word_of(fb) & valid_mask(nvb);
+            }
             if ((fla | flb) != 0u) {
-                if (fla != 0u) exact(fa, sna, fla, sa);
-                if (flb != 0u) exact(fb, snb, flb, sb);
+                if (fla != 0u) exact(fa, fla, sa);
+                if (flb != 0u) exact(fb, flb, sb);
             }
 
             // ---- online softmax for head n over this lane's 8 tokens.  The running max
@@ -444,10 +497,16 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 template <int D, int GW>
 void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
     constexpr int NB = VSPEC_I4_PAIRS_IN_FLIGHT;
-    if (p.block_tokens == 16) {
-        hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB>), grid, dim3(256), 0, s, p);
+    if (p.read_flags) {
+        if (p.block_tokens == 16)
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB, true>), grid, dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, true>), grid, dim3(256), 0, s, p);
     } else {
-        hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB>), grid, dim3(256), 0, s, p);
+        if (p.block_tokens == 16)
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB, false>), grid, dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, false>), grid, dim3(256), 0, s, p);
     }
 }
 

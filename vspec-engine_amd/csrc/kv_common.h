@@ -183,6 +183,8 @@ struct DecodeParams {
     const uint8_t* v;
     const uint16_t* ks;
     const uint16_t* vs;
+    const uint32_t* kf;  // int4 clamp flags [num_blocks][hkv][P/16] or null (a fused append keeps them)
+    bool read_flags;     // the decode takes the flags instead of screening every tile
     const int32_t* block_tables;
     const int32_t* ctx_lens;
     const float* q;

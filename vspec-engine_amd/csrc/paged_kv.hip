@@ -607,6 +607,8 @@ struct CompactParams {
     uint8_t* v;
     uint16_t* ks;
     uint16_t* vs;
+    uint32_t* kf;            // int4 clamp flags or null
+    uint32_t block_flags;    // flag words per physical block
     const int32_t* src;
     const int32_t* dst;
     uint32_t n;
@@ -636,6 +638,10 @@ __global__ __launch_bounds__(256) void kv_compact(CompactParams p) {
             const uint64_t jj = j < p.block_scales ? j : j - p.block_scales;
             base[(uint64_t)d * p.block_scales + jj] = base[(uint64_t)s * p.block_scales + jj];
         }
+    }
+    if (p.kf) {
+        for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < p.block_flags; j += gridDim.x * blockDim.x)
+            p.kf[(uint64_t)d * p.block_flags + j] = p.kf[(uint64_t)s * p.block_flags + j];
     }
 }
 
@@ -812,6 +818,16 @@ uint32_t decode_old_permille() {
     return x >= 500 && x <= 900 ? (uint32_t)x : kDefaultOldPermille;
 }
 
+// int4 clamp flags are read by the decode only when the balanced split gives each workgroup
+// at least this many tiles (VSPEC_ROCM_DECODE_FLAG_MIN_TILES, 0..4096); shorter shares read
+// no flags and screen every tile.  Read on every call.
+constexpr uint32_t kDefaultFlagMinTiles = 64;
+uint32_t decode_flag_min_tiles() {
+    const char* e = getenv("VSPEC_ROCM_DECODE_FLAG_MIN_TILES");
+    const long x = e ? strtol(e, nullptr, 10) : -1;
+    return x >= 0 && x <= 4096 ? (uint32_t)x : kDefaultFlagMinTiles;
+}
+
 struct DecodePlan {
     uint32_t gw;
     uint32_t gsplit;
@@ -822,6 +838,7 @@ struct DecodePlan {
     bool split;
     uint32_t grid_x;
     uint32_t chunk_tiles;
+    uint64_t split_tiles;  // tiles the balanced split spreads over grid_x (upper bound)
     uint32_t max_tiles;
 };
 
@@ -877,6 +894,7 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
             if (grid > bound) grid = bound;
         }
         pl->grid_x = (uint32_t)(grid ? grid : 1);
+        pl->split_tiles = bound;
         pl->max_tiles = max_tiles;
         pl->tiles_per_part = 0;
         pl->max_parts = 1;
@@ -959,7 +977,10 @@ size_t vspec_rocm_kv_pool_bytes(int32_t dtype, uint32_t num_blocks, uint32_t blo
                                 uint32_t num_kv_heads, uint32_t head_dim) {
     const size_t rows = (size_t)num_blocks * num_kv_heads * block_tokens;
     size_t bytes = 2 * rows * row_bytes_of(dtype, head_dim);
-    if (dtype == VSPEC_KV_INT4) bytes += 2 * rows * (head_dim / 32) * sizeof(uint16_t);
+    if (dtype == VSPEC_KV_INT4) {
+        bytes += 2 * rows * (head_dim / 32) * sizeof(uint16_t);
+        bytes += (rows / 16) * sizeof(uint32_t);  // clamp flags
+    }
     return bytes;
 }
 
@@ -992,9 +1013,12 @@ int vspec_rocm_kv_pool_create(VspecPagedKV* kv, int32_t dtype, uint32_t num_bloc
     }
     if (dtype == VSPEC_KV_INT4) {
         const size_t sb = rows * (head_dim / 32) * sizeof(uint16_t);
+        const size_t fb = (rows / 16) * sizeof(uint32_t);
         if (hipMalloc((void**)&kv->k_scales, sb) != hipSuccess ||
-            hipMalloc((void**)&kv->v_scales, sb) != hipSuccess) {
-            set_err("kv_pool_create: hipMalloc of scales failed");
+            hipMalloc((void**)&kv->v_scales, sb) != hipSuccess ||
+            hipMalloc((void**)&kv->k_flags, fb) != hipSuccess ||
+            hipMemset(kv->k_flags, 0, fb) != hipSuccess) {
+            set_err("kv_pool_create: hipMalloc of scales or flags failed");
             vspec_rocm_kv_pool_destroy(kv);
             return 0;
         }
@@ -1008,6 +1032,7 @@ void vspec_rocm_kv_pool_destroy(VspecPagedKV* kv) {
     if (kv->v_data) (void)hipFree(kv->v_data);
     if (kv->k_scales) (void)hipFree(kv->k_scales);
     if (kv->v_scales) (void)hipFree(kv->v_scales);
+    if (kv->k_flags) (void)hipFree(kv->k_flags);
     memset(kv, 0, sizeof(*kv));
 }
 
@@ -1017,6 +1042,7 @@ static int append_launch(const char* who, const VspecPagedKV* kv, AppendParams& 
     p.v = (uint8_t*)kv->v_data;
     p.ks = kv->k_scales;
     p.vs = kv->v_scales;
+    p.kf = kv->dtype == VSPEC_KV_INT4 ? kv->k_flags : nullptr;
     p.hkv = kv->num_kv_heads;
     p.head_dim = kv->head_dim;
     p.block_tokens = kv->block_tokens;
@@ -1220,6 +1246,8 @@ int vspec_rocm_kv_compact(const VspecPagedKV* kv, uint32_t n, const int32_t* src
     const uint64_t rows = (uint64_t)kv->num_kv_heads * kv->block_tokens;
     p.block_bytes = rows * row_bytes_of(kv->dtype, kv->head_dim);
     p.block_scales = kv->dtype == VSPEC_KV_INT4 ? rows * (kv->head_dim / 32) : 0;
+    p.kf = kv->dtype == VSPEC_KV_INT4 ? kv->k_flags : nullptr;
+    p.block_flags = (uint32_t)(rows / 16);
     uint64_t gx = (2 * (p.block_bytes / 16) + 255) / 256;
     if (gx > 64) gx = 64;
     if (gx == 0) gx = 1;
@@ -1324,6 +1352,8 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.v = (const uint8_t*)desc->kv.v_data;
     p.ks = desc->kv.k_scales;
     p.vs = desc->kv.v_scales;
+    p.kf = desc->kv.dtype == VSPEC_KV_INT4 ? desc->kv.k_flags : nullptr;
+    p.read_flags = p.kf && pl.split && pl.split_tiles >= (uint64_t)decode_flag_min_tiles() * pl.grid_x;
     p.block_tables = desc->block_tables;
     p.ctx_lens = desc->ctx_lens;
     p.q = desc->q;

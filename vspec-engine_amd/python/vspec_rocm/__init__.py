@@ -35,6 +35,7 @@ class VspecPagedKV(C.Structure):
         ("v_data", _vp),
         ("k_scales", _vp),
         ("v_scales", _vp),
+        ("k_flags", _vp),
     ]
 
 
@@ -235,9 +236,11 @@ def _stream(stream=None):
 class PagedPool:
     """A paged KV pool in HBM, owned by torch tensors, in the layout of
     include/vspec_rocm.h: K/V [num_blocks][H][P][D] (f32/f16) or codes
-    [num_blocks][H][P][D/2] plus fp16-bit scales [num_blocks][H][P][D/32] (int4)."""
+    [num_blocks][H][P][D/2] plus fp16-bit scales [num_blocks][H][P][D/32] (int4), and for
+    int4 the clamp flags [num_blocks][H][P/16] (flags=False: none, the decode screens keys)."""
 
-    def __init__(self, dtype: int, num_blocks: int, block_tokens: int, num_kv_heads: int, head_dim: int, device="cuda"):
+    def __init__(self, dtype: int, num_blocks: int, block_tokens: int, num_kv_heads: int, head_dim: int, device="cuda",
+                 flags=True):
         import torch
 
         self.dtype, self.num_blocks, self.block_tokens = dtype, num_blocks, block_tokens
@@ -256,8 +259,10 @@ class PagedPool:
         if dtype == KV_INT4:
             self.ks = torch.zeros((rows, head_dim // 32), dtype=torch.int16, device=device)
             self.vs = torch.zeros((rows, head_dim // 32), dtype=torch.int16, device=device)
+            self.kf = (torch.zeros((num_blocks * num_kv_heads * (block_tokens // 16),), dtype=torch.int32, device=device)
+                       if flags else None)
         else:
-            self.ks = self.vs = None
+            self.ks = self.vs = self.kf = None
 
     def desc(self) -> VspecPagedKV:
         d = VspecPagedKV()
@@ -265,6 +270,7 @@ class PagedPool:
         d.num_kv_heads, d.head_dim = self.num_kv_heads, self.head_dim
         d.k_data, d.v_data = self.k.data_ptr(), self.v.data_ptr()
         d.k_scales, d.v_scales = _ptr(self.ks), _ptr(self.vs)
+        d.k_flags = _ptr(self.kf)
         return d
 
 
