@@ -464,6 +464,9 @@ def main():
                                 "f32": "decode_partial" + (" + decode_combine" if ws_bytes else "")}[wl["dtype"]],
                      "algorithmic_bytes_per_launch": alg},
     }
+    if (Hq, Hkv, D) == (32, 8, 128):
+        # one step covers one layer; Qwen3-8B decodes a token through 36 of them
+        result["model_level"] = {"model": "Qwen3-8B", "layers": 36, "tokens_per_s": result["value"] / 36}
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         # the parity spot check compares against pool 0 (the timed loop rotates pools)

@@ -240,10 +240,10 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // Clamp screen of key n of a tile (this lane: one group's codes): mean and E[x^2]
         // from integer code sums; this group's |x| <= 8 * scale.  `flag` is set in a lane
         // whose group may reach the clamp threshold; key n is flagged when any of its four
-        // lanes is (tokens() folds the wave's ballot).  Pools with clamp flags skip it: the
+        // lanes is (tokens() folds the wave's ballot).  The flag kernel (FL) skips it: the
         // append ran the same test once per key (alpha 4.5; a larger alpha only clamps
-        // less), except in the tile that this launch's fused append wrote into, whose flag
-        // word the scalar cache may hold from before the write.
+        // less).  Only tiles this launch's fused append wrote into are screened there,
+        // except the one whose new flag the append published in LDS.
         struct Screen {
             float mean;
             bool flag;
