@@ -563,6 +563,8 @@ def test_decode_step_fused_append(oracle, gpu, flag_gate, dtype, Hq, Hkv, D, P, 
     for a, b in zip(pool_bytes(pools[0]), pool_bytes(pools[1])):
         if a is not None:
             assert np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+    if dtype == DTYPE_INT4:
+        assert torch.equal(pools[0].kf, pools[1].kf)  # the clamp flags as well
     assert_pools_equal(host, pools[1])
     assert torch.equal(got, want)
     full.host = host
