@@ -143,7 +143,8 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc);
  * with start_pos = ctx_lens - 1 and n_new = 1, then attends as
  * vspec_rocm_paged_decode_attention.  k_new, v_new: device [batch][num_kv_heads][head_dim]
  * in src_dtype (VSPEC_KV_F32 or VSPEC_KV_F16).  f16 and int4 pools do both in one kernel
- * launch; f32 pools launch the append first. */
+ * launch; f32 pools launch the append first.  A batch of 0 is a no-op returning 1 (k_new
+ * and v_new may then be NULL), as with every entry point here. */
 int vspec_rocm_paged_decode_step(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
                                  int32_t src_dtype);
 

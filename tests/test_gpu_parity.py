@@ -641,6 +641,50 @@ def test_decode_step_rejects_bad_source(gpu):
     assert "src_dtype" in vr.last_error()
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+def test_empty_batches_and_bad_arguments(gpu, dtype):
+    """Empty inputs are successful no-ops on every entry point (append, gather, compaction,
+    decode, decode step), whatever their pointers; bad decode arguments fail with 0 and a
+    message and leave the output as it was."""
+    import ctypes as C
+    import torch
+    import vspec_rocm as vr
+
+    say(f"[empty] dtype={dtype}")
+    L = vr.lib()
+    pool = vr.PagedPool(dtype, 4, 16, 2, 64, device=gpu)
+    kv = pool.desc()
+    assert L.vspec_rocm_kv_append(C.byref(kv), 0, None, 0, None, 1, None, None, vr.KV_F32, None) == 1
+    assert L.vspec_rocm_kv_append(C.byref(kv), 3, None, 0, None, 0, None, None, vr.KV_F32, None) == 1
+    assert L.vspec_rocm_kv_gather(C.byref(kv), 0, None, 0, None, 0, None, 0, None, None, None, None, None) == 1
+    assert L.vspec_rocm_kv_compact(C.byref(kv), 0, None, None, None) == 1
+    tab = torch.zeros((2, 4), dtype=torch.int32, device=gpu)
+    cl = torch.tensor([20, 5], dtype=torch.int32, device=gpu)
+    q = torch.randn((2, 4, 64), device=gpu)
+    out = torch.full_like(q, 7.0)
+    d = vr.make_decode_desc(pool, tab, cl, q, out, 20, vr.NUMERICS_3BIT)
+    d.batch = 0
+    assert L.vspec_rocm_paged_decode_attention(C.byref(d)) == 1
+    assert L.vspec_rocm_paged_decode_step(C.byref(d), None, None, vr.KV_F32) == 1
+    d.batch = 2
+    bad = [("numerics", 5, "numerics"), ("max_ctx_len", 65, "max_ctx_len"), ("num_q_heads", 3, "num_q_heads")]
+    for field, value, word in bad:
+        good = getattr(d, field)
+        setattr(d, field, value)
+        assert L.vspec_rocm_paged_decode_attention(C.byref(d)) == 0, field
+        assert word in vr.last_error()
+        setattr(d, field, good)
+    ws_need = vr.decode_workspace_bytes(d)
+    if ws_need:
+        small = torch.empty(ws_need - 1, dtype=torch.uint8, device=gpu)
+        d.workspace, d.workspace_bytes = small.data_ptr(), ws_need - 1
+        assert L.vspec_rocm_paged_decode_attention(C.byref(d)) == 0
+        assert "workspace" in vr.last_error()
+    assert L.vspec_rocm_paged_decode_attention(None) == 0
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+
+
 # ----------------------------------------------------------------------------- config 5
 @pytest.mark.parametrize("mode", [0, 1])
 def test_config5_chunk_evict_compact(oracle, gpu, flag_gate, mode):

@@ -1447,7 +1447,8 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
 
 int vspec_rocm_paged_decode_step(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
                                  int32_t src_dtype) {
-    if (!k_new || !v_new) {
+    const bool empty = desc && desc->batch == 0;  // a no-op, like every other entry point
+    if (!empty && (!k_new || !v_new)) {
         set_err("paged_decode_step: null k_new or v_new");
         return 0;
     }
