@@ -1185,7 +1185,7 @@ int vspec_rocm_kv_gather(const VspecPagedKV* kv, uint32_t batch, const int32_t* 
         set_err("kv_gather: int4 raw gather needs scale outputs");
         return 0;
     }
-    GatherParams p;
+    GatherParams p = {};
     p.k = (const uint8_t*)kv->k_data;
     p.v = (const uint8_t*)kv->v_data;
     p.ks = kv->k_scales;
@@ -1234,7 +1234,7 @@ int vspec_rocm_kv_compact(const VspecPagedKV* kv, uint32_t n, const int32_t* src
         set_err("kv_compact: null block list");
         return 0;
     }
-    CompactParams p;
+    CompactParams p = {};
     p.k = (uint8_t*)kv->k_data;
     p.v = (uint8_t*)kv->v_data;
     p.ks = kv->k_scales;
@@ -1264,7 +1264,7 @@ int vspec_rocm_kv_gather_rows(const VspecPagedKV* kv, uint32_t n, const int32_t*
         set_err("kv_gather_rows: null argument");
         return 0;
     }
-    GatherRowsParams p;
+    GatherRowsParams p = {};
     p.k = (const uint8_t*)kv->k_data;
     p.v = (const uint8_t*)kv->v_data;
     p.ks = kv->k_scales;
@@ -1347,7 +1347,7 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     const bool three = desc->numerics == VSPEC_NUMERICS_3BIT;
     if (three) scale = fminf(fmaxf(scale, 1e-4f), 32.0f);
 
-    DecodeParams p;
+    DecodeParams p = {};
     p.k = (const uint8_t*)desc->kv.k_data;
     p.v = (const uint8_t*)desc->kv.v_data;
     p.ks = desc->kv.k_scales;
