@@ -641,6 +641,76 @@ def test_decode_step_rejects_bad_source(gpu):
     assert "src_dtype" in vr.last_error()
 
 
+@pytest.mark.parametrize("shape,dtype", [("north-star", DTYPE_F16), ("north-star", DTYPE_INT4),
+                                         ("c4", DTYPE_F16)])
+def test_full_size_sampled_against_oracle(oracle, gpu, shape, dtype):
+    """The benchmark shapes at full size: north star (64 sequences x 4097 tokens, GQA
+    32/8, D=128; f16 and int4 pools, int4 through the clamp-flag kernel) and C4 (64
+    sequences, contexts U[128, 8192]).  The pool is filled on the GPU, the decode step
+    appends each sequence's last token and attends (mode R), then a plain decode runs
+    in mode P.  Four sampled sequences are gathered back (dequantised for int4), laid into
+    an fp32 oracle pool and decoded by the oracle: the GPU rows must agree within the
+    tolerance of the pool dtype."""
+    import torch
+    import vspec_rocm as vr
+
+    B, Hq, Hkv, D, P = 64, 32, 8, 128, 16
+    if shape == "north-star":
+        ctx = np.full(B, 4097, np.int32)
+    else:
+        ctx = np.random.default_rng(4).integers(128, 8193, B).astype(np.int32)
+    nb = (ctx + P - 1) // P
+    say(f"[full-size] {shape} dtype={dtype} tokens={int(ctx.sum())}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(1234 + dtype)
+    pool = vr.PagedPool(dtype, int(nb.sum()), P, Hkv, D, device=gpu)
+    perm = torch.randperm(int(nb.sum()), generator=g, device=gpu).to(torch.int32)
+    tab = torch.full((B, int(nb.max())), -1, dtype=torch.int32, device=gpu)
+    off = 0
+    for b in range(B):
+        tab[b, : nb[b]] = perm[off: off + nb[b]]
+        off += int(nb[b])
+    T = int(ctx.max())
+    for b in range(B):
+        # each sequence's context minus the decode token, in one append launch per sequence
+        n = int(ctx[b]) - 1
+        k = torch.randn((1, n, Hkv, D), generator=g, device=gpu).to(torch.float16)
+        v = torch.randn((1, n, Hkv, D), generator=g, device=gpu).to(torch.float16)
+        vr.kv_append(pool, tab[b: b + 1], torch.zeros(1, dtype=torch.int32, device=gpu), k, v)
+    kn = torch.randn((B, Hkv, D), generator=g, device=gpu).to(torch.float16)
+    vn = torch.randn((B, Hkv, D), generator=g, device=gpu).to(torch.float16)
+    q = torch.randn((B, Hq, D), generator=g, device=gpu)
+    cl = torch.from_numpy(ctx).to(gpu)
+    got = {1: vr.paged_decode_step(pool, tab, cl, q, kn, vn, max_ctx_len=T, numerics=1).cpu().numpy()}
+    got[0] = vr.paged_decode(pool, tab, cl, q, max_ctx_len=T, numerics=0).cpu().numpy()
+    torch.cuda.synchronize()
+    sample = np.array([0, 17, 42, 63])
+    st = torch.from_numpy(sample).to(gpu)
+    kf, vf, _, _ = vr.kv_gather(pool, tab[st], cl[st], out_mode=vr.GATHER_F32, max_ctx_len=T)
+    kf, vf = kf.cpu().numpy(), vf.cpu().numpy()
+    snb = nb[sample]
+    host = HostPool(DTYPE_F32, int(snb.sum()), P, Hkv, D)
+    htab = np.full((len(sample), int(snb.max())), -1, np.int32)
+    off = 0
+    for i, n in enumerate(snb):
+        htab[i, :n] = np.arange(off, off + n, dtype=np.int32)
+        off += int(n)
+    off = 0
+    for i, b in enumerate(sample):
+        n = int(ctx[b])
+        assert oracle.paged_append(host, htab[i: i + 1], np.zeros(1, np.int32),
+                                   np.ascontiguousarray(kf[off: off + n][None]),
+                                   np.ascontiguousarray(vf[off: off + n][None]))
+        off += n
+    qs = q.cpu().numpy()[sample]
+    for mode in (1, 0):
+        want = oracle.paged_decode(mode, host, htab, ctx[sample], qs)
+        err = np.abs(got[mode][sample] - want).max()
+        say(f"[full-size] mode={mode} max-abs {err:.2e}")
+        assert np.isfinite(got[mode]).all()
+        assert err <= TOL[dtype]
+
+
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
 def test_empty_batches_and_bad_arguments(gpu, dtype):
     """Empty inputs are successful no-ops on every entry point (append, gather, compaction,
