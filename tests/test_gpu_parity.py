@@ -641,6 +641,24 @@ def test_decode_step_rejects_bad_source(gpu):
     assert "src_dtype" in vr.last_error()
 
 
+def _oracle_decode_sampled(oracle, kf, vf, ctx, q, mode, P, Hkv, D):
+    """Oracle decode of gathered (f32) rows [sum(ctx)][Hkv][D] laid into an fp32 pool."""
+    nb = (ctx + P - 1) // P
+    host = HostPool(DTYPE_F32, int(nb.sum()), P, Hkv, D)
+    tab = np.full((len(ctx), int(nb.max())), -1, np.int32)
+    off = 0
+    for i, n in enumerate(nb):
+        tab[i, :n] = np.arange(off, off + n, dtype=np.int32)
+        off += int(n)
+    off = 0
+    for i, n in enumerate(ctx):
+        n = int(n)
+        assert oracle.paged_append(host, tab[i: i + 1], np.zeros(1, np.int32), np.ascontiguousarray(kf[off: off + n][None]),
+                                   np.ascontiguousarray(vf[off: off + n][None]))
+        off += n
+    return oracle.paged_decode(mode, host, tab, ctx, q)
+
+
 @pytest.mark.parametrize("shape,dtype", [("north-star", DTYPE_F16), ("north-star", DTYPE_INT4),
                                          ("c4", DTYPE_F16)])
 def test_full_size_sampled_against_oracle(oracle, gpu, shape, dtype):
@@ -688,27 +706,54 @@ def test_full_size_sampled_against_oracle(oracle, gpu, shape, dtype):
     st = torch.from_numpy(sample).to(gpu)
     kf, vf, _, _ = vr.kv_gather(pool, tab[st], cl[st], out_mode=vr.GATHER_F32, max_ctx_len=T)
     kf, vf = kf.cpu().numpy(), vf.cpu().numpy()
-    snb = nb[sample]
-    host = HostPool(DTYPE_F32, int(snb.sum()), P, Hkv, D)
-    htab = np.full((len(sample), int(snb.max())), -1, np.int32)
-    off = 0
-    for i, n in enumerate(snb):
-        htab[i, :n] = np.arange(off, off + n, dtype=np.int32)
-        off += int(n)
-    off = 0
-    for i, b in enumerate(sample):
-        n = int(ctx[b])
-        assert oracle.paged_append(host, htab[i: i + 1], np.zeros(1, np.int32),
-                                   np.ascontiguousarray(kf[off: off + n][None]),
-                                   np.ascontiguousarray(vf[off: off + n][None]))
-        off += n
     qs = q.cpu().numpy()[sample]
     for mode in (1, 0):
-        want = oracle.paged_decode(mode, host, htab, ctx[sample], qs)
+        want = _oracle_decode_sampled(oracle, kf, vf, ctx[sample], qs, mode, P, Hkv, D)
         err = np.abs(got[mode][sample] - want).max()
         say(f"[full-size] mode={mode} max-abs {err:.2e}")
         assert np.isfinite(got[mode]).all()
         assert err <= TOL[dtype]
+
+
+def test_config5_full_size_sampled(oracle, gpu):
+    """C5 at full size (8 int4 contexts of 16k-32k tokens, one 512-token fp16 chunk each,
+    oldest 25 % of blocks evicted, survivors compacted, decode in both modes), built on the
+    GPU; two sampled sequences are gathered back dequantised and decoded by the oracle."""
+    import torch
+    import vspec_rocm as vr
+    from cases import chunk_evict_c5
+
+    plan = chunk_evict_c5(oracle)
+    B, Hq, Hkv, D, P, chunk = 8, 32, 8, 128, 16, 512
+    say(f"[c5-full] contexts {plan['L0'].tolist()} -> {plan['new_ctx'].tolist()}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(55)
+    pool = vr.PagedPool(DTYPE_INT4, plan["num_blocks"], P, Hkv, D, device=gpu)
+    tab = torch.from_numpy(plan["tables"]).to(gpu)
+    for b in range(B):
+        n = int(plan["L0"][b])
+        k = torch.randn((1, n, Hkv, D), generator=g, device=gpu).to(torch.float16)
+        v = torch.randn((1, n, Hkv, D), generator=g, device=gpu).to(torch.float16)
+        vr.kv_append(pool, tab[b: b + 1], torch.zeros(1, dtype=torch.int32, device=gpu), k, v)
+    kc = torch.randn((B, chunk, Hkv, D), generator=g, device=gpu).to(torch.float16)
+    vc = torch.randn((B, chunk, Hkv, D), generator=g, device=gpu).to(torch.float16)
+    vr.kv_append(pool, tab, torch.from_numpy(plan["L0"]).to(gpu), kc, vc)
+    vr.kv_compact(pool, torch.from_numpy(plan["src"]).to(gpu), torch.from_numpy(plan["dst"]).to(gpu))
+    ntab = torch.from_numpy(plan["new_tables"]).to(gpu)
+    ncl = torch.from_numpy(plan["new_ctx"]).to(gpu)
+    q = torch.randn((B, Hq, D), generator=g, device=gpu)
+    T = int(plan["new_ctx"].max())
+    got = {m: vr.paged_decode(pool, ntab, ncl, q, max_ctx_len=T, numerics=m).cpu().numpy() for m in (1, 0)}
+    sample = np.array([0, 5])
+    st = torch.from_numpy(sample).to(gpu)
+    kf, vf, _, _ = vr.kv_gather(pool, ntab[st], ncl[st], out_mode=vr.GATHER_F32, max_ctx_len=T)
+    kf, vf = kf.cpu().numpy(), vf.cpu().numpy()
+    for mode in (1, 0):
+        want = _oracle_decode_sampled(oracle, kf, vf, plan["new_ctx"][sample], q.cpu().numpy()[sample], mode, P, Hkv, D)
+        err = np.abs(got[mode][sample] - want).max()
+        say(f"[c5-full] mode={mode} max-abs {err:.2e}")
+        assert np.isfinite(got[mode]).all()
+        assert err <= TOL[DTYPE_INT4]
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
