@@ -355,6 +355,72 @@ def test_int4_clamp_flags_are_conservative(oracle, gpu):
     assert clear >= 0.8 * (total - fired)
 
 
+def _attention_p_f64(q, keys, vals, alpha, scale):
+    """Mode P (attention_ref.c:7-88 with the 3-bit module off) in float64 with clamp
+    alpha `alpha`: q' = clamp(q), k' = clamp(k) per key, clamp(x) = clip(x, +-max(1e-6,
+    alpha * std(x))) around 0 (three_bit_runtime_modules.c:175-203), softmax of
+    scale * q'.k', output = p.v.  q [D]; keys, vals [T][D]."""
+    def clamp(x):
+        th = max(1e-6, alpha * float(np.sqrt(np.mean((x - x.mean()) ** 2))))
+        return np.clip(x, -th, th)
+
+    qc = clamp(q.astype(np.float64))
+    kc = np.stack([clamp(k) for k in keys.astype(np.float64)])
+    sc = (kc @ qc) * scale
+    w = np.exp(sc - sc.max())
+    return (w / w.sum()) @ vals.astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
+@pytest.mark.parametrize("alpha", [3.0, 6.0])
+def test_decode_custom_clamp_alpha(oracle, gpu, flag_gate, dtype, alpha):
+    """clamp_alpha other than the reference's 4.5 (mode P), on keys with outliers: below
+    4.5 the int4 decode screens every key (the pool's flags are kept for 4.5), above it
+    the flags stay a superset of the clamped keys.  Checked against a float64 restatement
+    over the pool's (dequantised) keys."""
+    import ctypes as C
+    import torch
+    import vspec_rocm as vr
+
+    say(f"[alpha] dtype={dtype} alpha={alpha}")
+    case = make_case(oracle, dtype, 2, 8, 2, 128, 16, [300, 130], seed=97, src16=False)
+    k = case.k_tokens.copy()
+    # outliers in pairs within one 32-element group, so that int4's scale (the group's
+    # second-largest |x|) keeps them
+    k[0, ::7, 0, 3:5] = 9.0
+    k[0, 1::9, 1, 50:52] = 4.2
+    k[1, ::5, 1, 100:102] = -6.0
+    k[1, 3, 0, :] *= 12.0
+    case.k_tokens = k
+    case.q = case.q.copy()
+    case.q[0, 2, 7] = 5.0
+    pool = build_both(oracle, case, gpu)
+    keys, vals, _, _ = oracle.paged_gather(case.host, case.tables, case.ctx, out_mode=1)
+    tab = torch.from_numpy(case.tables).to(gpu)
+    cl = torch.from_numpy(case.ctx).to(gpu)
+    q = torch.from_numpy(case.q).to(gpu)
+    out = torch.full_like(q, float("nan"))
+    d = vr.make_decode_desc(pool, tab, cl, q, out, case.tmax, vr.NUMERICS_PLAIN)
+    d.clamp_alpha = alpha
+    assert vr.lib().vspec_rocm_paged_decode_attention(C.byref(d)) == 1, vr.last_error()
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    scale = 1.0 / np.sqrt(case.D)
+    off, err, moved = 0, 0.0, 0.0
+    for b in range(case.B):
+        n = int(case.ctx[b])
+        for h in range(case.Hq):
+            kh = h // (case.Hq // case.Hkv)
+            want = _attention_p_f64(case.q[b, h], keys[off: off + n, kh], vals[off: off + n, kh], alpha, scale)
+            base = _attention_p_f64(case.q[b, h], keys[off: off + n, kh], vals[off: off + n, kh], 4.5, scale)
+            err = max(err, float(np.abs(got[b, h] - want).max()))
+            moved = max(moved, float(np.abs(want - base).max()))
+        off += n
+    say(f"[alpha] max-abs {err:.2e}; alpha moves the result by {moved:.2e}")
+    assert moved > 10 * TOL[dtype]  # the case does depend on alpha
+    assert err <= TOL[dtype]
+
+
 # ----------------------------------------------------------------------------- configs 2-4
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
 @pytest.mark.parametrize("mode", [0, 1])
