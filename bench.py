@@ -309,6 +309,10 @@ def main():
                          "to its step); the roofline averages the bracketed launches")
     ap.add_argument("--separate-append", action="store_true",
                     help="append with its own launch before the decode launch (timed: the decode)")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="override the workload's batch (uniform-context workloads only)")
+    ap.add_argument("--ctx", type=int, default=0,
+                    help="override the workload's context, decode token included (uniform only)")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="copy a buffer of this many MiB on the device once before warm-up, so that "
@@ -327,7 +331,12 @@ def main():
 
     vr.lib()
     dev = torch.device("cuda:0")
-    wl = WORKLOADS[args.workload]
+    wl = dict(WORKLOADS[args.workload])
+    if args.batch or args.ctx:
+        if "T" not in wl:
+            sys.exit("--batch / --ctx apply to uniform-context workloads only")
+        wl["B"] = args.batch or wl["B"]
+        wl["T"] = args.ctx or wl["T"]
     kv_dtype = {"f16": vr.KV_F16, "f32": vr.KV_F32, "int4": vr.KV_INT4}[wl["dtype"]]
     mode = vr.NUMERICS_3BIT if args.numerics == "R" else vr.NUMERICS_PLAIN
     if wl.get("flow") == "c5":

@@ -218,6 +218,9 @@ struct DecodeParams {
     // balanced split with a grid of two workgroups per CU: share of the first-half
     // workgroup of each (g, g + G/2) pair in 1/1000 (500: equal shares)
     uint32_t split_old_permille;
+    // least tiles per workgroup of the balanced split (>= 1), applied to the actual total
+    // so that the split does not depend on the host's bound
+    uint32_t min_tiles;
 };
 
 // Launch the MFMA decode kernels for f16 pools (decode_mfma.hip) and int4 pools
@@ -352,6 +355,7 @@ __device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r)
         r.hi = (int)min((long long)r.lo + p.chunk_tiles, (long long)r.total);
     } else {
         r.groups = min((int)gridDim.x, r.total);
+        if (p.min_tiles > 1) r.groups = min(r.groups, max(1, r.total / (int)p.min_tiles));
         // Unequal shares for ragged batches with at least 64 tiles per workgroup (measured:
         // C4 206 -> 190 us at 700; equal contexts lose, their ranges stop coinciding with
         // whole work items), and only where every second-half share is at least one tile:

@@ -818,6 +818,21 @@ uint32_t decode_old_permille() {
     return x >= 500 && x <= 900 ? (uint32_t)x : kDefaultOldPermille;
 }
 
+// Least tiles per workgroup of the balanced split: VSPEC_ROCM_DECODE_MIN_TILES_PER_WG
+// (1..256) when set, else 16 for batches of at most 8 work items and 1 otherwise.  With
+// 8 work items (one sequence, 8 kv heads) and a grid of 2 workgroups per CU, a 1k-4k
+// context leaves 1-4 tiles per workgroup and 64 partials per work item for its last
+// workgroup to merge (eight rounds of loads); 16 tiles per workgroup cut the int4 step at
+// B=1 from 30 to 21 us and the f16 one from 23 to 21 us.  At 16 work items the same floor
+// loses (f16 at 1k: 21 -> 26 us), and from 16k tokens on it makes no difference.  Read
+// on every call.
+uint32_t decode_min_tiles_per_wg(uint64_t items) {
+    const char* e = getenv("VSPEC_ROCM_DECODE_MIN_TILES_PER_WG");
+    const long x = e ? strtol(e, nullptr, 10) : 0;
+    if (x >= 1 && x <= 256) return (uint32_t)x;
+    return items <= 8 ? 16u : 1u;
+}
+
 // int4 clamp flags are read by the decode only when the balanced split gives each workgroup
 // at least this many tiles (VSPEC_ROCM_DECODE_FLAG_MIN_TILES, 0..4096); shorter shares read
 // no flags and screen every tile.  Read on every call.
@@ -839,6 +854,7 @@ struct DecodePlan {
     uint32_t grid_x;
     uint32_t chunk_tiles;
     uint64_t split_tiles;  // tiles the balanced split spreads over grid_x (upper bound)
+    uint32_t min_tiles;    // least tiles per workgroup of the balanced split
     uint32_t max_tiles;
 };
 
@@ -868,6 +884,7 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
     }
     const uint32_t max_tiles = (uint32_t)((ctx_bound + kTile - 1) / kTile);
     pl->split = d->kv.dtype != VSPEC_KV_F32;
+    pl->min_tiles = decode_min_tiles_per_wg((uint64_t)d->batch * hkv * pl->gsplit);
     if (pl->split) {
         // every workgroup streams an equal share of all work items' tiles
         const uint64_t bound = (uint64_t)d->batch * hkv * pl->gsplit * (max_tiles ? max_tiles : 1);
@@ -891,7 +908,10 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
             uint32_t wpc = decode_wgs_per_cu_env();
             if (!wpc) wpc = d->kv.dtype == VSPEC_KV_F16 && bound < 128ull * (uint64_t)num_cus() ? 1u : 2u;
             grid = (uint64_t)wpc * (uint64_t)num_cus();
-            if (grid > bound) grid = bound;
+            // the kernel caps its groups at total / min_tiles of the actual tiles; the grid
+            // (from the bound, which is at least the total) only trims idle workgroups
+            const uint64_t min_tiles = pl->min_tiles;
+            if (grid * min_tiles > bound) grid = bound / min_tiles;
         }
         pl->grid_x = (uint32_t)(grid ? grid : 1);
         pl->split_tiles = bound;
@@ -1384,6 +1404,7 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     const bool paired = pl.split && !pl.chunk_tiles && pl.grid_x == 2u * (uint32_t)num_cus() &&
                         desc->kv.dtype == VSPEC_KV_F16;
     p.split_old_permille = paired ? decode_old_permille() : 500u;
+    p.min_tiles = pl.split && !pl.chunk_tiles ? pl.min_tiles : 1u;
 
     hipStream_t s = (hipStream_t)desc->stream;
     if (k_new) {
