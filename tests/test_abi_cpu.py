@@ -151,3 +151,31 @@ def test_abi_types_match_reference_headers(tmp_path):
     ours = _probe('#include "vspec_abi.h"', "", INC, tmp_path, "ours_abi")
     theirs = _probe('#include "vspec/kernel/backend.h"\n#include "vspec/attention/kv_cache.h"', "", REF_INC, tmp_path, "ref_abi")
     assert ours == theirs
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """With the HIP library absent the binding raises on first use, high-level calls
+    included: there is no CPU fallback to run instead."""
+    import os
+    import sys
+
+    code = (
+        "import torch\n"
+        "import vspec_rocm as vr\n"
+        "pool = vr.PagedPool(vr.KV_F16, 2, 16, 1, 64, device='cpu')\n"
+        "tab = torch.zeros((1, 2), dtype=torch.int32)\n"
+        "sp = torch.zeros(1, dtype=torch.int32)\n"
+        "k = torch.zeros((1, 1, 1, 64), dtype=torch.float16)\n"
+        "for f in (vr.lib, lambda: vr.kv_append(pool, tab, sp, k, k)):\n"
+        "    try:\n"
+        "        f()\n"
+        "    except vr.VspecRocmError as e:\n"
+        "        assert 'missing' in str(e)\n"
+        "    else:\n"
+        "        raise SystemExit('no error')\n"
+        "print('raised')\n"
+    )
+    env = dict(os.environ, VSPEC_ROCM_LIB=str(tmp_path / "absent.so"),
+               PYTHONPATH=str(ROOT / "vspec-engine_amd" / "python"))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "raised" in r.stdout, r.stderr[-2000:]
