@@ -421,6 +421,58 @@ def test_decode_custom_clamp_alpha(oracle, gpu, flag_gate, dtype, alpha):
     assert err <= TOL[dtype]
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_decode_random_shapes(oracle, gpu, seed):
+    """Seeded random shapes against the oracle: pool dtype, batch 1-12, kv heads 1/2/4/8,
+    GQA group 1/2/3/4/8, head_dim 64/128, block 16/32/48/64 tokens, ragged contexts of
+    0-700 tokens, numerics P/R, and the plain decode or the fused decode step (whose
+    appended token the oracle appends too)."""
+    import torch
+    import vspec_rocm as vr
+
+    rng = np.random.default_rng(9000 + seed)
+    dtype = [DTYPE_F32, DTYPE_F16, DTYPE_INT4][seed % 3]
+    B = int(rng.integers(1, 13))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    grp = int(rng.choice([1, 2, 3, 4, 8]))
+    D = int(rng.choice([64, 128]))
+    P = int(rng.choice([16, 32, 48, 64]))
+    ctx = rng.integers(0, 701, B).astype(np.int32)
+    ctx[rng.random(B) < 0.15] = 0
+    mode = int(rng.integers(0, 2))
+    step = bool(rng.integers(0, 2)) and dtype != DTYPE_F32
+    say(f"[random {seed}] dtype={dtype} B={B} Hkv={Hkv} group={grp} D={D} P={P} mode={mode} step={step} "
+        f"ctx={ctx.tolist()}")
+    case = make_case(oracle, dtype, B, Hkv * grp, Hkv, D, P, ctx, seed=300 + seed,
+                     num_blocks=int(((ctx + P - 1) // P).sum()) + 3)
+    if step:
+        # build the pool without each sequence's last token; the decode step appends it
+        full_ctx = case.ctx
+        case.ctx = np.maximum(full_ctx - 1, 0).astype(np.int32)
+        pool = build_both(oracle, case, gpu)
+        case.ctx = full_ctx
+        last = np.maximum(full_ctx - 1, 0)
+        kn = np.ascontiguousarray(case.k_tokens[np.arange(B), last])
+        vn = np.ascontiguousarray(case.v_tokens[np.arange(B), last])
+        live = np.flatnonzero(full_ctx > 0)
+        if live.size:
+            assert oracle.paged_append(case.host, np.ascontiguousarray(case.tables[live]),
+                                       (full_ctx[live] - 1).astype(np.int32),
+                                       np.ascontiguousarray(kn[live][:, None]), np.ascontiguousarray(vn[live][:, None]))
+        out = vr.paged_decode_step(pool, torch.from_numpy(case.tables).to(gpu), torch.from_numpy(full_ctx).to(gpu),
+                                   torch.from_numpy(case.q).to(gpu), _np_to_dev(kn, gpu), _np_to_dev(vn, gpu),
+                                   max_ctx_len=case.tmax, numerics=mode)
+        torch.cuda.synchronize()
+        assert_pools_equal(case.host, pool)
+        got = out.cpu().numpy()
+    else:
+        pool = build_both(oracle, case, gpu)
+        got = run_decode(case, pool, gpu, mode)
+    empty = np.flatnonzero(case.ctx == 0)
+    assert np.all(got[empty] == 0.0)
+    check_attention(oracle, case, got, mode, subset=np.flatnonzero(case.ctx > 0))
+
+
 # ----------------------------------------------------------------------------- configs 2-4
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
 @pytest.mark.parametrize("mode", [0, 1])
