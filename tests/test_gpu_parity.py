@@ -425,8 +425,9 @@ def test_decode_custom_clamp_alpha(oracle, gpu, flag_gate, dtype, alpha):
 def test_decode_random_shapes(oracle, gpu, seed):
     """Seeded random shapes against the oracle: pool dtype, batch 1-12, kv heads 1/2/4/8,
     GQA group 1/2/3/4/8, head_dim 64/128, block 16/32/48/64 tokens, ragged contexts of
-    0-700 tokens, numerics P/R, and the plain decode or the fused decode step (whose
-    appended token the oracle appends too)."""
+    0-700 tokens, numerics P/R, and the plain decode (with a random split-K partition
+    size and max_ctx_len, the true bound or 0) or the fused decode step (whose appended
+    token the oracle appends too)."""
     import torch
     import vspec_rocm as vr
 
@@ -441,8 +442,10 @@ def test_decode_random_shapes(oracle, gpu, seed):
     ctx[rng.random(B) < 0.15] = 0
     mode = int(rng.integers(0, 2))
     step = bool(rng.integers(0, 2)) and dtype != DTYPE_F32
+    pt = int(rng.choice([0, 0, 16, 32, 48]))       # split-K partition tokens (plain decode)
+    cap = bool(rng.integers(0, 2))                  # max_ctx_len 0: the block table's capacity
     say(f"[random {seed}] dtype={dtype} B={B} Hkv={Hkv} group={grp} D={D} P={P} mode={mode} step={step} "
-        f"ctx={ctx.tolist()}")
+        f"pt={pt} cap={cap} ctx={ctx.tolist()}")
     case = make_case(oracle, dtype, B, Hkv * grp, Hkv, D, P, ctx, seed=300 + seed,
                      num_blocks=int(((ctx + P - 1) // P).sum()) + 3)
     if step:
@@ -467,7 +470,11 @@ def test_decode_random_shapes(oracle, gpu, seed):
         got = out.cpu().numpy()
     else:
         pool = build_both(oracle, case, gpu)
-        got = run_decode(case, pool, gpu, mode)
+        out = vr.paged_decode(pool, torch.from_numpy(case.tables).to(gpu), torch.from_numpy(case.ctx).to(gpu),
+                              torch.from_numpy(case.q).to(gpu), max_ctx_len=0 if cap else case.tmax,
+                              numerics=mode, partition_tokens=pt)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
     empty = np.flatnonzero(case.ctx == 0)
     assert np.all(got[empty] == 0.0)
     check_attention(oracle, case, got, mode, subset=np.flatnonzero(case.ctx > 0))
