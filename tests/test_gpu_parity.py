@@ -245,6 +245,53 @@ def test_compact_bitexact(oracle, gpu):
     assert_pools_equal(case.host, pool)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_append_gather_compact_random(oracle, gpu, seed):
+    """Seeded random shapes for the byte-exact part of the path: the appended pool (f32 /
+    f16 sources, ragged contexts, block sizes 16-64), the raw and dequantised gathers, and
+    a compaction of a random subset of the used blocks into free ones, all equal to the
+    oracle's bytes."""
+    import torch
+    import vspec_rocm as vr
+
+    rng = np.random.default_rng(7000 + seed)
+    dtype = [DTYPE_F32, DTYPE_F16, DTYPE_INT4][seed % 3]
+    B = int(rng.integers(1, 9))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    D = int(rng.choice([64, 128]))
+    P = int(rng.choice([16, 32, 48, 64]))
+    src16 = bool(rng.integers(0, 2))
+    ctx = rng.integers(0, 400, B).astype(np.int32)
+    used_blocks = int(((ctx + P - 1) // P).sum())
+    nblk = used_blocks + int(rng.integers(used_blocks // 2 + 1, used_blocks + 3))
+    say(f"[bytes {seed}] dtype={dtype} B={B} Hkv={Hkv} D={D} P={P} src16={src16} blocks={nblk} ctx={ctx.tolist()}")
+    case = make_case(oracle, dtype, B, Hkv, Hkv, D, P, ctx, seed=400 + seed, num_blocks=nblk, src16=src16)
+    pool = build_both(oracle, case, gpu)
+    assert_pools_equal(case.host, pool)
+    tab = torch.from_numpy(case.tables).to(gpu)
+    cl = torch.from_numpy(case.ctx).to(gpu)
+    for mode in (vr.GATHER_RAW, vr.GATHER_F32):
+        got = vr.kv_gather(pool, tab, cl, out_mode=mode, max_ctx_len=max(case.tmax, 1))
+        want = oracle.paged_gather(case.host, case.tables, case.ctx, out_mode=mode)
+        for g_, w_ in zip(got, want):
+            if w_ is None:
+                assert g_ is None
+                continue
+            g_ = g_.cpu().numpy()
+            assert np.array_equal(np.ascontiguousarray(g_).view(np.uint8).reshape(-1),
+                                  np.ascontiguousarray(w_).view(np.uint8).reshape(-1))
+    used = case.tables[case.tables >= 0]
+    if used.size:
+        free = np.setdiff1d(np.arange(nblk, dtype=np.int32), used)
+        k = int(min(free.size, rng.integers(1, used.size + 1)))
+        src = rng.permutation(used)[:k].astype(np.int32)
+        dst = rng.permutation(free)[:k].astype(np.int32)
+        assert oracle.paged_compact(case.host, src, dst)
+        vr.kv_compact(pool, torch.from_numpy(src).to(gpu), torch.from_numpy(dst).to(gpu))
+        torch.cuda.synchronize()
+        assert_pools_equal(case.host, pool)
+
+
 # ----------------------------------------------------------------------------- decode edge cases
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
 @pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 8), (128, 8, 4), (128, 16, 4), (128, 16, 2), (64, 6, 2)])
