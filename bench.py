@@ -11,10 +11,16 @@ synthetic (seeded N(0,1)) and resident in HBM before timing starts.
 Printed JSON (one line on stdout):
   value      whole-step tokens/s = batch * steps / wall seconds
   roofline   the decode kernel: algorithmic bytes per launch (with the fused
-             append's bytes) / the average launch time from HIP events on the
-             launch stream, against 8 TB/s
+             append's bytes) / the average launch time, from one pair of HIP events
+             on the launch stream around all timed launches, against 8 TB/s; and
+             against the measured ceilings of lib/libvspec_probe.so: a streaming
+             copy (copy_gbs) and a read of 4 KB tiles in random order with the
+             decode kernels' non-temporal loads (read_tiles_gbs)
   cpu_baseline  the reference's own C path (oracle/_ref: append + capi gather +
              attention_ref) timed on a bounded sample of the same workload
+
+--probe prints the bandwidth probes alone (copy, random and sequential 4 KB tile reads
+with ordinary and non-temporal loads).
 """
 from __future__ import annotations
 
@@ -117,17 +123,93 @@ def cpu_baseline(args, wl, pool, tables, ctx, q_all, out_gpu, mode):
 
 
 def host_cpu():
-    """The host the CPU baseline ran on: model name (as lscpu prints it) and usable threads."""
+    """The host the CPU baseline ran on: the model name lscpu prints (else /proc/cpuinfo's)
+    and the usable threads."""
+    import subprocess
+
     model = ""
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
         pass
+    if not model:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        model = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
     return {"cpu_model": model, "nproc": len(os.sched_getaffinity(0))}
+
+
+PROBE_LIB = ROOT / "vspec-engine_amd" / "lib" / "libvspec_probe.so"
+
+
+def probe_ceilings(dev, gib=1, reps=10):
+    """Measured HBM ceilings from lib/libvspec_probe.so, each timed with one event pair
+    around `reps` launches after two warm-up launches on torch's current stream:
+      copy_gbs        streaming copy of `gib` GiB (2 x size bytes moved per launch)
+      read_tiles_gbs  2 * gib GiB read as 4 KB tiles in a random order, non-temporal loads
+                      (the decode kernels' access pattern and load policy)
+      read_tiles_cached_gbs  the same with ordinary loads
+      read_seq_gbs    the tiles in order, non-temporal loads"""
+    import ctypes as C
+
+    import torch
+
+    if not PROBE_LIB.exists():
+        raise FileNotFoundError(f"{PROBE_LIB} is missing: build it with __graft_entry__.build()")
+    P = C.CDLL(str(PROBE_LIB))
+    P.vspec_probe_copy.restype = C.c_int
+    P.vspec_probe_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+    P.vspec_probe_read_tiles.restype = C.c_int
+    P.vspec_probe_read_tiles.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int,
+                                         C.c_void_p]
+    P.vspec_probe_read_tiles_grid.restype = C.c_uint32
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def timed(launch, nbytes):
+        for _ in range(2):
+            assert launch()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            assert launch()
+        b.record()
+        torch.cuda.synchronize()
+        return nbytes * reps / (a.elapsed_time(b) / 1e3) / 1e9
+
+    n = gib << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.random_(0, 256)
+    res = {"copy_gbs": timed(lambda: P.vspec_probe_copy(src.data_ptr(), dst.data_ptr(), n, stream), 2 * n)}
+    del src, dst
+    tile = 4096
+    buf = torch.empty(2 * n, dtype=torch.uint8, device=dev)
+    buf.random_(0, 256)
+    ntiles = (2 * n) // tile
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    perm = torch.randperm(ntiles, generator=g, device=dev).to(torch.int32)
+    seq = torch.arange(ntiles, dtype=torch.int32, device=dev)
+    sink = torch.empty(P.vspec_probe_read_tiles_grid() * 256, dtype=torch.int32, device=dev)
+    rd = lambda tab, nt: (lambda: P.vspec_probe_read_tiles(buf.data_ptr(), tab.data_ptr(), ntiles, tile,
+                                                           sink.data_ptr(), nt, stream))
+    res["read_tiles_gbs"] = timed(rd(perm, 1), 2 * n)
+    res["read_tiles_cached_gbs"] = timed(rd(perm, 0), 2 * n)
+    res["read_seq_gbs"] = timed(rd(seq, 1), 2 * n)
+    del buf, perm, seq, sink
+    torch.cuda.synchronize()
+    res["probe"] = (f"lib/libvspec_probe.so: copy of {gib} GiB; reads of {2 * gib} GiB as 4 KB tiles; "
+                    f"{reps} launches per figure between one event pair")
+    return res
 
 
 def cpu_baseline_ragged(wl, pool, tables, ctx, q_all, out_gpu, mode, S, lens):
@@ -304,9 +386,13 @@ def main():
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--cpu-seqs", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--event-every", type=int, default=4,
-                    help="bracket every Nth timed launch with a HIP event pair (each pair adds ~7 us "
-                         "to its step); the roofline averages the bracketed launches")
+    ap.add_argument("--launch-samples", type=int, default=20,
+                    help="after the timed steps, time this many single launches between event pairs "
+                         "for the per-launch distribution (p10/median/p90; not part of value)")
+    ap.add_argument("--probe", action="store_true",
+                    help="print the HBM bandwidth probes (copy, random/sequential tile reads) and exit")
+    ap.add_argument("--no-probe", action="store_true",
+                    help="skip the probe ceilings in the bench line")
     ap.add_argument("--separate-append", action="store_true",
                     help="append with its own launch before the decode launch (timed: the decode)")
     ap.add_argument("--batch", type=int, default=0,
@@ -331,6 +417,10 @@ def main():
 
     vr.lib()
     dev = torch.device("cuda:0")
+    if args.probe:
+        print(json.dumps({"metric": "HBM bandwidth probes", "unit": "GB/s", "peak": PEAK_GBS,
+                          **probe_ceilings(dev), **{"host": host_cpu()}}), flush=True)
+        return
     wl = dict(WORKLOADS[args.workload])
     if args.batch or args.ctx:
         if "T" not in wl:
@@ -405,16 +495,12 @@ def main():
         d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
     L = vr.lib()
 
-    every = max(1, args.event_every)
-
-    def step(i):
+    def step(i, ev=None):
         c = i % copies
-        if args.separate_append:
-            vr.kv_append(pools[c], tables_l[c], pos, k_new, v_new)
-        ev = evs[i // every] if i >= 0 and i % every == 0 else None
         if ev:
             ev[0].record()
         if args.separate_append:
+            vr.kv_append(pools[c], tables_l[c], pos, k_new, v_new)
             ok = L.vspec_rocm_paged_decode_attention(C.byref(descs[c]))
         else:
             ok = L.vspec_rocm_paged_decode_step(C.byref(descs[c]), k_new.data_ptr(), v_new.data_ptr(), vr.KV_F16)
@@ -424,25 +510,33 @@ def main():
             ev[1].record()
 
     calibration_copy(args, dev)
-    evs = [None] * 0
     for i in range(args.warmup):
-        step(-1 - i)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range((args.steps + every - 1) // every)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
         step(i)
     torch.cuda.synchronize()
+    # one event pair on the launch stream (torch's current stream, which the descriptors
+    # name) around all timed launches
+    span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    t0 = time.perf_counter()
+    span[0].record()
+    for i in range(args.steps):
+        step(i)
+    span[1].record()
+    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    attn_ms = [a.elapsed_time(b) for a, b in evs]
-    attn_ms.sort()
-    avg_attn_s = sum(attn_ms) / len(attn_ms) / 1e3
-    med_attn_ms = attn_ms[len(attn_ms) // 2]
+    avg_attn_s = span[0].elapsed_time(span[1]) / args.steps / 1e3
+    # per-launch distribution, outside the timed region
+    samples = []
+    for i in range(max(0, args.launch_samples)):
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        step(i, ev)
+        torch.cuda.synchronize()
+        samples.append(ev[0].elapsed_time(ev[1]))
+    samples.sort()
+    pct = lambda f: samples[min(len(samples) - 1, int(f * len(samples)))] if samples else None
 
-    alg = algorithmic_bytes(lens, Hq, Hkv, D, P, wl["dtype"])
-    if not args.separate_append:
-        alg += step_append_bytes(B, Hkv, D, wl["dtype"])
+    # the step's append bytes count in both modes (fused: the same launch; separate: the
+    # append launch sits inside the event span too)
+    alg = algorithmic_bytes(lens, Hq, Hkv, D, P, wl["dtype"]) + step_append_bytes(B, Hkv, D, wl["dtype"])
     achieved = alg / avg_attn_s / 1e9
     traffic = load_traffic(args.workload)
 
@@ -464,15 +558,26 @@ def main():
                    "head_dim": D, "block_tokens": P, "kv_storage": wl["dtype"], "numerics": args.numerics,
                    "append": "separate launch" if args.separate_append else "fused into the decode launch",
                    "pool_copies": copies, "parallelism": "single-gpu"},
-        "decode_launch": {"launches_timed": len(attn_ms), "every": every,
-                          "tokens_per_s": B / avg_attn_s, "avg_ms": avg_attn_s * 1e3, "median_ms": med_attn_ms,
-                           "p10_ms": attn_ms[len(attn_ms) // 10], "p90_ms": attn_ms[(9 * len(attn_ms)) // 10]},
+        "decode_launch": {"timing": f"one event pair around the {args.steps} timed launches",
+                          "tokens_per_s": B / avg_attn_s, "avg_ms": avg_attn_s * 1e3,
+                          "single_launch_samples": len(samples), "median_ms": pct(0.5), "p10_ms": pct(0.1),
+                          "p90_ms": pct(0.9)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": traffic,
-                     "kernel": {"f16": "decode_mfma_f16", "int4": "decode_mfma_i4",
+                     "kernel": ("kv_append + " if args.separate_append else "") +
+                               {"f16": "decode_mfma_f16", "int4": "decode_mfma_i4",
                                 "f32": "decode_partial" + (" + decode_combine" if ws_bytes else "")}[wl["dtype"]],
                      "algorithmic_bytes_per_launch": alg},
     }
+    if not args.no_probe:
+        log("probe ceilings ...")
+        pc = probe_ceilings(dev)
+        rf = result["roofline"]
+        rf["copy_gbs"] = pc["copy_gbs"]
+        rf["frac_of_copy"] = achieved / pc["copy_gbs"]
+        rf["read_tiles_gbs"] = pc["read_tiles_gbs"]
+        rf["frac_of_read_tiles"] = achieved / pc["read_tiles_gbs"]
+        rf["probe"] = pc["probe"]
     if (Hq, Hkv, D) == (32, 8, 128):
         # one step covers one layer; Qwen3-8B decodes a token through 36 of them
         result["model_level"] = {"model": "Qwen3-8B", "layers": 36, "tokens_per_s": result["value"] / 36}

@@ -148,6 +148,11 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc);
 int vspec_rocm_paged_decode_step(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
                                  int32_t src_dtype);
 
+/* Free the library workspaces that later, larger decodes replaced on the current device.
+ * They are kept until this call because a captured HIP graph may still use them; call it
+ * only when no such graph will be replayed again. */
+int vspec_rocm_release_retired_workspaces(void);
+
 /* ---- misc ---- */
 int vspec_rocm_sync(void* stream);
 const char* vspec_rocm_last_error(void);

@@ -98,10 +98,11 @@ int vspec_rocm_paged_plan_step(VspecRocmPagedMeta* m, const VspecRocmStepItem* i
 
 /* Append packed new tokens (device pointers): token t of k_new/v_new ([n][H][D] in
  * src_dtype) goes to position token_pos[t] of the sequence whose block table is row
- * token_item[t] of block_tables.  Mixed chunked-prefill and decode steps append in
- * one launch; quantises on write for int4 pools. */
+ * token_item[t] of block_tables ([n_items][max_blocks_per_seq]); tokens whose item is
+ * negative or not below n_items are skipped.  Mixed chunked-prefill and decode steps
+ * append in one launch; quantises on write for int4 pools. */
 int vspec_rocm_kv_append_tokens(const VspecPagedKV* kv, uint32_t n_tokens, const int32_t* token_item,
-                                const int32_t* token_pos, const int32_t* block_tables,
+                                const int32_t* token_pos, const int32_t* block_tables, uint32_t n_items,
                                 uint32_t max_blocks_per_seq, const void* k_new, const void* v_new,
                                 int32_t src_dtype, void* stream);
 

@@ -1,11 +1,16 @@
 """GPU parity: the HIP path (through the C-ABI) against the CPU oracle on the same
 seeded inputs.
 
-Bars (BASELINE.json north star):
+Bars:
   * append, gather, compaction and int4 codes/scales: bit-exact;
-  * attention: max-abs 1e-4 with fp32 KV, 4e-3 with fp16 / int4 KV (fp32 accumulate),
-    in both reference numerics modes (P: 3-bit module off, R: on).
+  * attention, in both reference numerics modes (P: 3-bit module off, R: on): max-abs
+    2e-5 with fp32 and fp16 KV, and 2.5e-4 * max|v| + 2e-5 (capped at 4e-3) with int4 KV,
+    whose kernel rounds p * scale to fp16 once per token (relative 2^-12).  These are
+    tighter than the north-star bars (1e-4 fp32, 4e-3 fp16/int4): at 4k-token contexts a
+    single token carries ~2.5e-4 of the softmax weight, so a token dropped or read stale
+    by a merge or the fused append would pass the north-star bars unnoticed.
 """
+import ctypes as C
 import sys
 
 import numpy as np
@@ -15,7 +20,20 @@ from oracle.oracle import DTYPE_F16, DTYPE_F32, DTYPE_INT4, HostPool, _f32p, _u8
 from cases import GARBAGE, continuous_c4, fill_garbage, make_case, qwen_c2
 
 pytestmark = pytest.mark.gpu
-TOL = {DTYPE_F32: 1e-4, DTYPE_F16: 4e-3, DTYPE_INT4: 4e-3}
+TOL = {DTYPE_F32: 2e-5, DTYPE_F16: 2e-5, DTYPE_INT4: 4e-3}
+
+
+def tol_of(dtype, vmax=None):
+    """Max-abs bound of a decode against the oracle; int4 scales with max|v| (an upper
+    bound of the dequantised values when taken over the source values)."""
+    if dtype != DTYPE_INT4 or vmax is None:
+        return TOL[dtype]
+    return min(4e-3, 2.5e-4 * float(vmax) + 2e-5)
+
+
+def case_vmax(case):
+    v = case.v_tokens
+    return float(np.abs(v.view(np.float16) if v.dtype == np.uint16 else v).astype(np.float32).max())
 
 
 def say(*a):
@@ -168,8 +186,9 @@ def check_attention(oracle, case, got, mode, subset=None):
     want = oracle.paged_decode(mode, case.host, case.tables[idx], case.ctx[idx], case.q[idx])
     err = np.abs(got[idx] - want)
     assert np.isfinite(got[idx]).all()
-    tol = TOL[case.dtype]
-    assert err.max() <= tol, f"max-abs {err.max():.3e} > {tol:.0e} (mode {mode})"
+    tol = tol_of(case.dtype, case_vmax(case))
+    say(f"    max-abs {err.max():.2e} (bound {tol:.1e}, mode {mode})")
+    assert err.max() <= tol, f"max-abs {err.max():.3e} > {tol:.1e} (mode {mode})"
     return float(err.max())
 
 
@@ -465,7 +484,7 @@ def test_decode_custom_clamp_alpha(oracle, gpu, flag_gate, dtype, alpha):
         off += n
     say(f"[alpha] max-abs {err:.2e}; alpha moves the result by {moved:.2e}")
     assert moved > 10 * TOL[dtype]  # the case does depend on alpha
-    assert err <= TOL[dtype]
+    assert err <= tol_of(dtype, case_vmax(case))
 
 
 @pytest.mark.parametrize("seed", range(24))
@@ -628,11 +647,11 @@ def test_decode_partition_invariance(oracle, gpu):
 
 
 def test_decode_back_to_back_and_streams(oracle, gpu):
-    """Split work items are merged in-kernel through per-(device, stream) arrival
-    counters that every launch returns to zero: decodes of different shapes and dtypes
-    back to back on one stream, then on two streams at once with their own workspaces,
-    must all reproduce the first run bit for bit (every output row written: the output
-    is NaN-filled before each launch)."""
+    """Split work items leave partial states in the workspace for the merge launch that
+    follows on the same stream: decodes of different shapes and dtypes back to back on one
+    stream, then on two streams at once with their own workspaces, must all reproduce the
+    first run bit for bit (every output row written: the output is NaN-filled before each
+    launch)."""
     import torch
     import vspec_rocm as vr
 
@@ -798,6 +817,111 @@ def test_decode_step_in_hip_graph(oracle, gpu, flag_gate, dtype):
         run_decode(other, pool_o, gpu, 1)
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
+def test_decode_step_new_token_dominates(oracle, gpu, flag_gate, dtype):
+    """Long contexts (4097 tokens, each work item split over several workgroups) where the
+    decode step's own token carries almost all of the softmax weight of one query head per
+    group: its key is twice that head's query.  Leaving the token out, or reading its tile
+    before the fused append's stores, moves that head's output by O(1); the fused step and
+    the separate append + decode must both match the oracle within the tight bound."""
+    import copy
+
+    import torch
+    import vspec_rocm as vr
+
+    say(f"[dominant token] dtype={dtype}")
+    B, Hq, Hkv, D, P, T = 8, 32, 8, 128, 16, 4097
+    full = make_case(oracle, dtype, B, Hq, Hkv, D, P, [T] * B, seed=303 + dtype)
+    grp = Hq // Hkv
+    k = full.k_tokens.copy()
+    qf = full.q.reshape(B, Hkv, grp, D)[:, :, 0, :]  # first query head of each group
+    k[:, T - 1] = oracle.f32_to_f16((2.0 * qf).astype(np.float32))
+    full.k_tokens = k
+    pre = copy.copy(full)
+    pre.ctx = np.full(B, T - 1, np.int32)
+    pre.host = HostPool(dtype, full.num_blocks, P, Hkv, D)
+    fill_garbage(pre.host)
+    pools = [build_both(oracle, pre, gpu)]
+    pre2 = copy.copy(pre)
+    pre2.host = HostPool(dtype, full.num_blocks, P, Hkv, D)
+    fill_garbage(pre2.host)
+    pools.append(build_both(oracle, pre2, gpu))
+    host = pre.host
+    k_new = np.ascontiguousarray(k[:, T - 1])
+    v_new = np.ascontiguousarray(full.v_tokens[:, T - 1])
+    assert oracle.paged_append(host, full.tables, np.full(B, T - 1, np.int32), np.ascontiguousarray(k_new[:, None]),
+                               np.ascontiguousarray(v_new[:, None]))
+    full.host = host
+    tab = torch.from_numpy(full.tables).to(gpu)
+    cl = torch.from_numpy(full.ctx).to(gpu)
+    q = torch.from_numpy(full.q).to(gpu)
+    kd, vd = _np_to_dev(k_new, gpu), _np_to_dev(v_new, gpu)
+    for mode in (1, 0):
+        got = vr.paged_decode_step(pools[0], tab, cl, q, kd, vd, max_ctx_len=T, numerics=mode).cpu().numpy()
+        check_attention(oracle, full, got, mode)
+        # the new token does dominate: without it the first head of each group moves by O(1)
+        without = oracle.paged_decode(mode, pre2.host, full.tables, pre.ctx, full.q)
+        assert np.abs(got - without).reshape(B, Hkv, grp, D)[:, :, 0].max() > 0.1
+    vr.kv_append(pools[1], tab, cl - 1, kd[:, None].contiguous(), vd[:, None].contiguous())
+    got = vr.paged_decode(pools[1], tab, cl, q, max_ctx_len=T, numerics=1).cpu().numpy()
+    check_attention(oracle, full, got, 1)
+
+
+def test_graph_replay_survives_workspace_growth(oracle, gpu):
+    """A decode captured into a HIP graph with the library's own workspace; then an eager
+    decode on the same stream that needs a larger workspace makes the library replace it.
+    The replaced buffer is retired, not freed, so later replays of the graph still match
+    the eager result bit for bit; the retired buffer is released afterwards."""
+    import torch
+    import vspec_rocm as vr
+
+    say("[graph + growth] build")
+    small = make_case(oracle, DTYPE_F16, 4, 4, 2, 64, 16, [900, 33, 1601, 257], seed=91)
+    # head_dim 128 and 4 heads per work item need about four times the small step's
+    # partial-state workspace; 600 sequences x 8 kv heads = 4,800 work items to merge
+    big = make_case(oracle, DTYPE_F16, 600, 32, 8, 128, 16, [20 + (i % 13) for i in range(600)], seed=92)
+    pool_s = build_both(oracle, small, gpu)
+    pool_b = build_both(oracle, big, gpu)
+    tab = torch.from_numpy(small.tables).to(gpu)
+    cl = torch.from_numpy(small.ctx).to(gpu)
+    q = torch.from_numpy(small.q).to(gpu)
+    out = torch.full_like(q, float("nan"))
+    s = torch.cuda.Stream()
+
+    def step():
+        vr.paged_decode(pool_s, tab, cl, q, max_ctx_len=small.tmax, numerics=1, out=out, stream=s.cuda_stream)
+
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
+    want = out.clone()
+    check_attention(oracle, small, want.cpu().numpy(), 1)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    tab_b = torch.from_numpy(big.tables).to(gpu)
+    cl_b = torch.from_numpy(big.ctx).to(gpu)
+    q_b = torch.from_numpy(big.q).to(gpu)
+    for rep in range(3):
+        if rep == 1:
+            say("[graph + growth] larger eager decode on the capture stream")
+            with torch.cuda.stream(s):
+                got_b = vr.paged_decode(pool_b, tab_b, cl_b, q_b, max_ctx_len=big.tmax, numerics=1,
+                                        stream=s.cuda_stream)
+            torch.cuda.synchronize()
+            check_attention(oracle, big, got_b.cpu().numpy(), 1, subset=[0, 1, 299, 599])
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep}"
+    # the caller may free the retired buffers once no graph that uses them will run again
+    del g
+    torch.cuda.synchronize()
+    assert vr.lib().vspec_rocm_release_retired_workspaces() == 1, vr.last_error()
+
+
 def test_decode_step_rejects_bad_source(gpu):
     import torch
     import vspec_rocm as vr
@@ -882,9 +1006,10 @@ def test_full_size_sampled_against_oracle(oracle, gpu, shape, dtype):
     for mode in (1, 0):
         want = _oracle_decode_sampled(oracle, kf, vf, ctx[sample], qs, mode, P, Hkv, D)
         err = np.abs(got[mode][sample] - want).max()
-        say(f"[full-size] mode={mode} max-abs {err:.2e}")
+        tol = tol_of(dtype, np.abs(vf).max())
+        say(f"[full-size] mode={mode} max-abs {err:.2e} (bound {tol:.1e})")
         assert np.isfinite(got[mode]).all()
-        assert err <= TOL[dtype]
+        assert err <= tol
 
 
 def test_config5_full_size_sampled(oracle, gpu):
@@ -923,9 +1048,10 @@ def test_config5_full_size_sampled(oracle, gpu):
     for mode in (1, 0):
         want = _oracle_decode_sampled(oracle, kf, vf, plan["new_ctx"][sample], q.cpu().numpy()[sample], mode, P, Hkv, D)
         err = np.abs(got[mode][sample] - want).max()
-        say(f"[c5-full] mode={mode} max-abs {err:.2e}")
+        tol = tol_of(DTYPE_INT4, np.abs(vf).max())
+        say(f"[c5-full] mode={mode} max-abs {err:.2e} (bound {tol:.1e})")
         assert np.isfinite(got[mode]).all()
-        assert err <= TOL[DTYPE_INT4]
+        assert err <= tol
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
@@ -1035,8 +1161,10 @@ def test_config5_chunk_evict_compact(oracle, gpu, flag_gate, mode):
     torch.cuda.synchronize()
     want = oracle.paged_decode(mode, host, plan["new_tables"], plan["new_ctx"], q)
     err = float(np.abs(out.cpu().numpy() - want).max())
-    assert err <= TOL[DTYPE_INT4], err
-    say(f"[c5] max-abs {err:.2e}")
+    scales = host.vs.view(np.float16).astype(np.float32)
+    tol = tol_of(DTYPE_INT4, 8.0 * np.abs(scales[np.isfinite(scales)]).max())  # |code| <= 8
+    say(f"[c5] max-abs {err:.2e} (bound {tol:.1e})")
+    assert err <= tol, err
 
 
 # ----------------------------------------------------------------------------- fused rotary + append

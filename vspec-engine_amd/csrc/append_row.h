@@ -19,6 +19,7 @@ struct AppendParams {
     // position token_pos[b] of block-table row token_item[b]
     const int32_t* token_item;
     const int32_t* token_pos;
+    uint32_t n_items;  // block-table rows in packed-token mode
     // rotary embedding of K (rope_cos != null): rows [max_pos][rope_dim / 2]
     const float* rope_cos;
     const float* rope_sin;

@@ -434,7 +434,6 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         cursor_next(p, ips, pc);
         reset();
     }
-    arrive_partials<D, GW>(p, ws, split_sh, ips, first, pc);
 }
 
 #ifndef VSPEC_F16_TILES_IN_FLIGHT
@@ -449,6 +448,9 @@ void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
     } else {
         hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0, NB>), grid, dim3(256), 0, s, p);
     }
+    // items split over several workgroups (same split: the f16 kernel's pair shares)
+    const dim3 merge_grid(p.batch * p.hkv * p.gsplit);
+    hipLaunchKernelGGL((decode_merge_split<D, GW, true>), merge_grid, dim3(kWaves * 64), 0, s, p);
 }
 
 template <int D>

@@ -484,8 +484,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             }
         }
         __syncthreads();
-        finish_segment<D, GW>(p, comb, ws, split_sh, b, hq0, b * ips + y, item0, U, tile_begin, tile_end,
-                              pos == ws.lo ? 0 : 1);
+        finish_segment<D, GW>(p, comb, b, hq0, U, tile_begin, tile_end, pos == ws.lo ? 0 : 1);
         pos = item0 + tile_end;
     }
 }
@@ -508,6 +507,9 @@ void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
         else
             hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, false>), grid, dim3(256), 0, s, p);
     }
+    // items split over several workgroups (same split: equal shares)
+    const dim3 merge_grid(p.batch * p.hkv * p.gsplit);
+    hipLaunchKernelGGL((decode_merge_split<D, GW, false>), merge_grid, dim3(kWaves * 64), 0, s, p);
 }
 
 template <int D>

@@ -205,7 +205,7 @@ struct DecodeParams {
     float input_clip;  // 16 in 3-bit mode, +inf otherwise
     // split of the MFMA kernels (see WorkSplit): part_ml / part_acc then hold two
     // partial slots per workgroup, [grid][2][GW][2] and [grid][2][GW][D]
-    uint32_t* arrivals;    // [batch * hkv * gsplit]; zero between launches
+    uint32_t split_grid;   // workgroups of the split kernel's grid (the merge launch redoes the split)
     uint32_t batch;
     uint32_t max_tiles;    // tiles of the host's context bound (max_ctx_len)
     uint32_t chunk_tiles;  // tiles per workgroup, or 0: split evenly over gridDim.x
@@ -224,8 +224,8 @@ struct DecodeParams {
 };
 
 // Launch the MFMA decode kernels for f16 pools (decode_mfma.hip) and int4 pools
-// (decode_mfma_int4.hip); they return 0 when no instantiation matches (head_dim,
-// heads per work item).
+// (decode_mfma_int4.hip), each followed by its merge launch (decode_merge_split); they
+// return 0 when no instantiation matches (head_dim, heads per work item).
 int launch_decode_mfma_f16(const DecodeParams& p, uint32_t head_dim, uint32_t gw, dim3 grid,
                            hipStream_t stream);
 int launch_decode_mfma_int4(const DecodeParams& p, uint32_t head_dim, uint32_t gw, dim3 grid,
@@ -273,14 +273,16 @@ __device__ __forceinline__ void merge_waves(const DecodeParams& p, const float (
 // U_b = max(1, min(ceil(ctx_b / 16), max_tiles)) tiles.  The tiles of all work items
 // are laid end to end, sequence-major in ctx_lens order with the hkv * gsplit items of
 // a sequence adjacent, T tiles in all.  Workgroup g takes the tiles [lo_g, lo_{g+1}):
-//   balanced  lo_g = floor(g * T / G), G = min(gridDim.x, T)
+//   balanced  lo_g = floor(g * T / G), G = min(split_grid, T)
 //   chunked   lo_g = g * chunk_tiles
 // so every workgroup streams the same number of tiles whatever the context lengths.
 // A work item that lies inside one workgroup's range goes straight to the output; one
 // that spans several leaves one partial (max, sum, acc) per workgroup, in slot 0 when
-// it is that workgroup's first segment and slot 1 when its last, and the workgroup that
-// arrives last at the item's counter merges them and resets the counter.  No
-// workgroup ever waits for another.
+// it is that workgroup's first segment and slot 1 when its last.  A second launch on the
+// same stream (decode_merge_split) merges them: it redoes the split from ctx_lens and
+// merges every item whose tiles meet more than one workgroup's range.  The kernel
+// boundary orders the partial stores before the merge's loads, so no workgroup waits
+// for or signals another, and no device state outlives a launch.
 // ---------------------------------------------------------------------------
 // Block tables and context lengths do not change while a decode kernel runs.  Read
 // through the constant address space, their wave-uniform reads stay scalar loads even
@@ -304,9 +306,9 @@ struct SplitShared {
     int wsum[kWaves];
     int umin[kWaves];  // per wave: least and greatest tiles per work item (U_b)
     int umax[kWaves];
+    int wpre[kWaves];  // merge launch: per wave, tiles of the sequences before the item's
     int b;
     int seq0;
-    int last[2];
 };
 
 __device__ __forceinline__ int item_tiles(const DecodeParams& p, int b) {
@@ -343,30 +345,39 @@ __device__ __forceinline__ int split_group_of(const DecodeParams& p, const WorkS
     return w.half + (int)((n - a * w.half - 1) / ((long long)(1000 - w.wa) * w.total));
 }
 
-// this workgroup's tiles [lo, hi) once T is known
+// The split's shape once T (and whether the batch is ragged) is known: groups and pair
+// shares.  The same for every workgroup of the split kernel and for the merge launch.
 template <bool UNEVEN>
-__device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r) {
-    const int g = blockIdx.x;
+__device__ __forceinline__ void split_shape(const DecodeParams& p, WorkSplit& r) {
+    const int grid = (int)p.split_grid;
     r.half = 0;
     r.wa = 500;
     if (p.chunk_tiles) {
         r.groups = 0;
+        return;
+    }
+    r.groups = min(grid, r.total);
+    if (p.min_tiles > 1) r.groups = min(r.groups, max(1, r.total / (int)p.min_tiles));
+    // Unequal shares for ragged batches with at least 64 tiles per workgroup (measured:
+    // C4 206 -> 190 us at 700; equal contexts lose, their ranges stop coinciding with
+    // whole work items), and only where every second-half share is at least one tile
+    // (every workgroup of an item's span then holds one of its partials).
+    if (UNEVEN && p.split_old_permille != 500 && r.ragged && r.groups == grid && (grid & 1) == 0 &&
+        (long long)r.total >= 64LL * grid && (long long)(1000 - (int)p.split_old_permille) * r.total >= 500LL * grid) {
+        r.half = grid / 2;
+        r.wa = (int)p.split_old_permille;
+    }
+}
+
+// this workgroup's tiles [lo, hi) once T is known
+template <bool UNEVEN>
+__device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r) {
+    const int g = blockIdx.x;
+    split_shape<UNEVEN>(p, r);
+    if (p.chunk_tiles) {
         r.lo = (int)min((long long)g * p.chunk_tiles, (long long)r.total);
         r.hi = (int)min((long long)r.lo + p.chunk_tiles, (long long)r.total);
     } else {
-        r.groups = min((int)gridDim.x, r.total);
-        if (p.min_tiles > 1) r.groups = min(r.groups, max(1, r.total / (int)p.min_tiles));
-        // Unequal shares for ragged batches with at least 64 tiles per workgroup (measured:
-        // C4 206 -> 190 us at 700; equal contexts lose, their ranges stop coinciding with
-        // whole work items), and only where every second-half share is at least one tile:
-        // an empty range inside a work item's span of workgroups would never count its
-        // arrival.
-        if (UNEVEN && p.split_old_permille != 500 && r.ragged && r.groups == (int)gridDim.x && (gridDim.x & 1) == 0 &&
-            (long long)r.total >= 64LL * gridDim.x &&
-            (long long)(1000 - (int)p.split_old_permille) * r.total >= 500LL * gridDim.x) {
-            r.half = (int)gridDim.x / 2;
-            r.wa = (int)p.split_old_permille;
-        }
         r.lo = g < r.groups ? split_lo<UNEVEN>(p, r, g) : r.total;
         r.hi = g < r.groups ? split_lo<UNEVEN>(p, r, g + 1) : r.total;
     }
@@ -503,17 +514,6 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
     return r;
 }
 
-// Partials cross workgroups that may sit on different XCDs, whose L2 caches are not
-// coherent with each other.  They are stored and loaded with device-scope accesses,
-// which write through to / read from the device's coherence point, so neither side
-// needs an agent-scope fence (a write-back or invalidation of the whole L2).
-__device__ __forceinline__ void store_device(float* ptr, float v) {
-    __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_device(const float* ptr) {
-    return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Position in the sequence-major order of work items (all fields wave-uniform).  Work
 // item y of sequence b covers kv head y / gsplit and query heads GW*y .. GW*y + GW - 1.
 struct ItemCursor {
@@ -573,125 +573,21 @@ __device__ __forceinline__ void merge_segment(const DecodeParams& p, const float
         if (whole) {
             p.out[(row0 + h) * D + d] = l > 0.f ? a / l : 0.f;
         } else {
-            store_device(pacc + idx, a);
+            pacc[idx] = a;
             if (d == 0) {
-                store_device(pml + 2 * h, M);
-                store_device(pml + 2 * h + 1, l);
+                pml[2 * h] = M;
+                pml[2 * h + 1] = l;
             }
         }
     }
 }
 
-// Block-wide, last arrival at work item c: merge the partials of the workgroups g0..g1
-// whose ranges meet its tiles, NBATCH workgroups per batch with all of a batch's loads
-// in flight together (a chain of one load at a time would cost a memory latency each).
-template <int D, int GW, bool UNEVEN>
-__device__ __forceinline__ void merge_group(const DecodeParams& p, const WorkSplit& w, const ItemCursor& c,
-                                            int tid) {
-    constexpr int NT = kWaves * 64;
-    constexpr int K = (GW * D + NT - 1) / NT;  // outputs per thread: idx = tid + NT * k
-    constexpr int NBATCH = 8;
-    const int g0 = split_group_of<UNEVEN>(p, w, c.item0);
-    const int g1 = split_group_of<UNEVEN>(p, w, c.item0 + c.U - 1);
-    const int first_inside = split_lo<UNEVEN>(p, w, g0) < c.item0 ? 1 : 0;
-    // running merge per output in log2 units; -1e30 (not -inf) keeps exp2 finite
-    float M[K], A[K], Ls[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        M[k] = -1e30f;
-        A[k] = 0.f;
-        Ls[k] = 0.f;
-    }
-    for (int g = g0; g <= g1; g += NBATCH) {
-        float mb[NBATCH][K], lb[NBATCH][K], ab[NBATCH][K];
-#pragma unroll
-        for (int i = 0; i < NBATCH; ++i) {
-            const bool valid = g + i <= g1;
-            const int gg = valid ? g + i : g1;
-            const size_t slot = (size_t)gg * 2 + (gg == g0 ? first_inside : 0);
-#pragma unroll
-            for (int k = 0; k < K; ++k) {
-                const int idx = min(tid + NT * k, GW * D - 1);
-                const int h = idx / D;
-                const int d = idx % D;
-                const float m = load_device(p.part_ml + (slot * GW + h) * 2);
-                const float l = load_device(p.part_ml + (slot * GW + h) * 2 + 1);
-                const float a = load_device(p.part_acc + (slot * GW + h) * D + d);
-                mb[i][k] = valid ? m : -1e30f;
-                lb[i][k] = valid ? l : 0.f;
-                ab[i][k] = valid ? a : 0.f;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < NBATCH; ++i) {
-#pragma unroll
-            for (int k = 0; k < K; ++k) {
-                const float nm = fmaxf(M[k], mb[i][k]);
-                const float fo = exp2f(M[k] - nm);
-                const float fn = exp2f(mb[i][k] - nm);
-                A[k] = fmaf(ab[i][k], fn, A[k] * fo);
-                Ls[k] = fmaf(lb[i][k], fn, Ls[k] * fo);
-                M[k] = nm;
-            }
-        }
-    }
-    const size_t row0 = (size_t)c.b * p.hq + (size_t)c.y * GW;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int idx = tid + NT * k;
-        if (idx < GW * D) p.out[(row0 + idx / D) * D + idx % D] = Ls[k] > 0.f ? A[k] / Ls[k] : 0.f;
-    }
-}
-
-// Block-wide, after every wave has merged its segments: count this workgroup's partials
-// (at most two: its first segment `first` and its last `last`) at their work items; the
-// workgroup that arrives last at an item merges all of the item's partials.
+// Block-wide: merge the kWaves per-wave states of one segment (tiles [tile_begin,
+// tile_end) of a work item of U tiles) and write the output rows when the segment is the
+// whole item, else the workgroup's partial `slot` for the merge launch.
 template <int D, int GW>
-__device__ __forceinline__ void arrive_partials(const DecodeParams& p, const WorkSplit& w, SplitShared& sh, int ips,
-                                                const ItemCursor& first, const ItemCursor& last) {
-    const bool part0 = !(first.item0 >= w.lo && first.item0 + first.U <= w.hi);
-    const bool part1 = last.item0 != first.item0 && !(last.item0 >= w.lo && last.item0 + last.U <= w.hi);
-    if (!part0 && !part1) return;
-    int tid = (int)threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    // every wave's partial stores have completed (they write through to the device's
-    // coherence point, so no L2 write-back is needed) before the arrivals are counted
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    // both arrivals at once: thread k counts item k (first, last)
-    if (tid < 2) {
-        const bool has = tid == 0 ? part0 : part1;
-        const int b = tid == 0 ? first.b : last.b;
-        const int y = tid == 0 ? first.y : last.y;
-        const int U = tid == 0 ? first.U : last.U;
-        const int item0 = tid == 0 ? first.item0 : last.item0;
-        int last_in = 0;
-        if (has) {
-            // the workgroups whose ranges meet the item's tiles [item0, item0 + U)
-            const int g0 = split_group_of<true>(p, w, item0);
-            const int g1 = split_group_of<true>(p, w, item0 + U - 1);
-            const uint32_t item = (uint32_t)(b * ips + y);
-            const uint32_t seen = atomicAdd(p.arrivals + item, 1u);
-            last_in = seen == (uint32_t)(g1 - g0);
-            if (last_in) __hip_atomic_store(p.arrivals + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        sh.last[tid] = last_in;
-    }
-    __syncthreads();
-    const int merge0 = sh.last[0];
-    const int merge1 = sh.last[1];
-    if (merge0) merge_group<D, GW, true>(p, w, first, tid);
-    if (merge1) merge_group<D, GW, true>(p, w, last, tid);
-}
-
-// Merge the kWaves per-wave states of one segment (tiles [tile_begin, tile_end) of the
-// work item `item`, whose U tiles start at global tile item0) and write the output row,
-// or the partial and, in the last workgroup to arrive, the merged output row.
-template <int D, int GW>
-__device__ __forceinline__ void finish_segment(const DecodeParams& p, const float (*comb)[GW][D + 2],
-                                               const WorkSplit& w, SplitShared& sh, int b, int hq0,
-                                               int item, int item0, int U, int tile_begin, int tile_end,
-                                               int slot) {
+__device__ __forceinline__ void finish_segment(const DecodeParams& p, const float (*comb)[GW][D + 2], int b,
+                                               int hq0, int U, int tile_begin, int tile_end, int slot) {
     const bool whole = tile_begin == 0 && tile_end == U;
     const size_t row0 = (size_t)b * p.hq + hq0;
     // thread index behind an opaque copy: the address arithmetic below then stays here
@@ -717,36 +613,127 @@ __device__ __forceinline__ void finish_segment(const DecodeParams& p, const floa
         if (whole) {
             p.out[(row0 + h) * D + d] = l > 0.f ? a / l : 0.f;
         } else {
-            store_device(pacc + idx, a);
+            pacc[idx] = a;
             if (d == 0) {
-                store_device(pml + 2 * h, M);
-                store_device(pml + 2 * h + 1, l);
+                pml[2 * h] = M;
+                pml[2 * h + 1] = l;
             }
         }
     }
-    if (whole) return;
-    // the workgroups whose ranges meet [item0, item0 + U)
-    const int g0 = split_group_of<false>(p, w, item0);
-    const int g1 = split_group_of<false>(p, w, item0 + U - 1);
-    // this wave's partial stores have completed (they write through to the device's
-    // coherence point, so no L2 write-back is needed) before the arrival is counted
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t seen = atomicAdd(p.arrivals + item, 1u);
-        const int last = seen == (uint32_t)(g1 - g0);
-        if (last) __hip_atomic_store(p.arrivals + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sh.last[0] = last;
+}
+
+// Merge launch of a split decode: one workgroup per work item (grid = batch * hkv *
+// gsplit, 256 threads).  It redoes the split kernel's split from ctx_lens (the same T,
+// groups and pair shares), and for an item whose tiles meet the ranges of workgroups
+// g0 < g1 it merges their partials in order g0..g1 and writes the item's output rows;
+// items inside one range were written by the split kernel and are left alone.  Partial
+// loads go out NBATCH workgroups at a time, all in flight together.
+template <int D, int GW, bool UNEVEN>
+__global__ __launch_bounds__(kWaves * 64) void decode_merge_split(DecodeParams p) {
+    constexpr int NT = kWaves * 64;
+    constexpr int K = (GW * D + NT - 1) / NT;  // outputs per thread: idx = tid + NT * k
+    constexpr int NBATCH = 8;
+    __shared__ SplitShared sh;
+    const int ips = (int)(p.hkv * p.gsplit);
+    const int b = (int)blockIdx.x / ips;
+    const int y = (int)blockIdx.x % ips;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nb = (int)p.batch;
+    // T, ragged and the tiles of the sequences before b, block-wide
+    int s = 0, pre = 0, umin = 0x7fffffff, umax = 0;
+    for (int i = threadIdx.x; i < nb; i += NT) {
+        const int u = item_tiles(p, i);
+        s += u;
+        pre += i < b ? u : 0;
+        umin = min(umin, u);
+        umax = max(umax, u);
+    }
+#pragma unroll
+    for (int o = 32; o; o >>= 1) {
+        s += __shfl_xor(s, o);
+        pre += __shfl_xor(pre, o);
+        umin = min(umin, __shfl_xor(umin, o));
+        umax = max(umax, __shfl_xor(umax, o));
+    }
+    if (lane == 0) {
+        sh.wsum[wave] = s;
+        sh.wpre[wave] = pre;
+        sh.umin[wave] = umin;
+        sh.umax[wave] = umax;
     }
     __syncthreads();
-    if (!sh.last[0]) return;
-    ItemCursor c;
-    c.b = b;
-    c.y = (int)(hq0 / GW);
-    c.U = U;
-    c.item0 = item0;
-    c.seq0 = 0;
-    merge_group<D, GW, false>(p, w, c, tid);
+    WorkSplit w;
+    int all = 0;
+    pre = 0;
+    umin = 0x7fffffff;
+    umax = 0;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) {
+        all += sh.wsum[v];
+        pre += sh.wpre[v];
+        umin = min(umin, sh.umin[v]);
+        umax = max(umax, sh.umax[v]);
+    }
+    w.total = all * ips;
+    w.ragged = UNEVEN && umin != umax ? 1 : 0;
+    split_shape<UNEVEN>(p, w);
+    const int U = item_tiles(p, b);
+    const int item0 = pre * ips + y * U;
+    const int g0 = split_group_of<UNEVEN>(p, w, item0);
+    const int g1 = split_group_of<UNEVEN>(p, w, item0 + U - 1);
+    if (g0 == g1) return;  // written by the split kernel
+    // the item is g0's last segment (slot 1) when g0's range starts before it, and the
+    // first segment (slot 0) of every later workgroup
+    const int first_inside = split_lo<UNEVEN>(p, w, g0) < item0 ? 1 : 0;
+    const int tid = (int)threadIdx.x;
+    // running merge per output in log2 units; -1e30 (not -inf) keeps exp2 finite
+    float M[K], A[K], Ls[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        M[k] = -1e30f;
+        A[k] = 0.f;
+        Ls[k] = 0.f;
+    }
+    for (int g = g0; g <= g1; g += NBATCH) {
+        float mb[NBATCH][K], lb[NBATCH][K], ab[NBATCH][K];
+#pragma unroll
+        for (int i = 0; i < NBATCH; ++i) {
+            const bool valid = g + i <= g1;
+            const int gg = valid ? g + i : g1;
+            const size_t slot = (size_t)gg * 2 + (gg == g0 ? first_inside : 0);
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const int idx = min(tid + NT * k, GW * D - 1);
+                const int h = idx / D;
+                const int d = idx % D;
+                const float m = p.part_ml[(slot * GW + h) * 2];
+                const float l = p.part_ml[(slot * GW + h) * 2 + 1];
+                const float a = p.part_acc[(slot * GW + h) * D + d];
+                mb[i][k] = valid ? m : -1e30f;
+                lb[i][k] = valid ? l : 0.f;
+                ab[i][k] = valid ? a : 0.f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NBATCH; ++i) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const float nm = fmaxf(M[k], mb[i][k]);
+                const float fo = exp2f(M[k] - nm);
+                const float fn = exp2f(mb[i][k] - nm);
+                A[k] = fmaf(ab[i][k], fn, A[k] * fo);
+                Ls[k] = fmaf(lb[i][k], fn, Ls[k] * fo);
+                M[k] = nm;
+            }
+        }
+    }
+    const size_t row0 = (size_t)b * p.hq + (size_t)y * GW;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int idx = tid + NT * k;
+        if (idx < GW * D) p.out[(row0 + idx / D) * D + idx % D] = Ls[k] > 0.f ? A[k] / Ls[k] : 0.f;
+    }
 }
 
 }  // namespace vkv

@@ -18,6 +18,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <vector>
 
 #include "vspec_rocm_paged.h"
 
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
             const int32_t cl = p.ctx_lens[b];
             sp = cl > 0 ? cl - 1 : -1;
         }
-        if (sp < 0 || item < 0) continue;
+        if (sp < 0 || item < 0 || (p.token_item && (uint32_t)item >= p.n_items)) continue;
         const size_t src_el = (((size_t)b * p.n_new + i) * p.hkv + h) * p.head_dim + (size_t)c * EPT;
         append_chunk<DT, SRC>(p, (uint32_t)item, (uint32_t)sp + i, h, c, which, src_el);
     }
@@ -710,14 +711,18 @@ int check_kv(const VspecPagedKV* kv, const char* who, bool decode = false) {
     return 1;
 }
 
-// grow-only library workspace per device (used when the caller passes none); the mutex
+// Grow-only library workspace per device (used when the caller passes none); the mutex
 // keeps host threads that decode on one device from growing it at the same time (its
-// contents are shared: concurrent decodes need workspaces of their own)
+// contents are shared: concurrent decodes need workspaces of their own).  A buffer that
+// is outgrown is retired, not freed: a HIP graph captured from an earlier decode still
+// holds its address, and replays must find it allocated.  Retired buffers are freed by
+// vspec_rocm_release_retired_workspaces() or at process exit.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
 Workspace g_ws[64];
+std::vector<void*> g_retired[64];
 std::mutex g_ws_mu;
 
 void* library_workspace(size_t bytes) {
@@ -726,75 +731,12 @@ void* library_workspace(size_t bytes) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace& w = g_ws[dev];
     if (w.bytes >= bytes) return w.ptr;
-    if (w.ptr) (void)hipFree(w.ptr);
-    w.ptr = nullptr;
-    w.bytes = 0;
-    if (hipMalloc(&w.ptr, bytes) != hipSuccess) {
-        w.ptr = nullptr;
-        return nullptr;
-    }
+    void* fresh = nullptr;
+    if (hipMalloc(&fresh, bytes) != hipSuccess) return nullptr;
+    if (w.ptr) g_retired[dev].push_back(w.ptr);
+    w.ptr = fresh;
     w.bytes = bytes;
     return w.ptr;
-}
-
-// Arrival counters of the MFMA decode split: one zeroed array per (device, stream),
-// grow-only.  Every launch returns the counters it used to zero, so a stream's array
-// stays valid for any later shape; launches on different streams never share one.
-struct Arrivals {
-    hipStream_t stream = nullptr;
-    uint32_t* ptr = nullptr;
-    size_t count = 0;
-    bool used = false;
-};
-constexpr int kArrivalStreams = 32;
-Arrivals g_arrivals[64][kArrivalStreams];
-std::mutex g_arrivals_mu;
-
-__global__ void fill_zero_u32(uint32_t* p, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = 0u;
-}
-
-uint32_t* arrival_counters(size_t count, hipStream_t stream) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-        set_err("paged_decode: no current device");
-        return nullptr;
-    }
-    std::lock_guard<std::mutex> lock(g_arrivals_mu);
-    Arrivals* slot = nullptr;
-    Arrivals* free_slot = nullptr;
-    for (Arrivals& a : g_arrivals[dev]) {
-        if (a.used && a.stream == stream) slot = &a;
-        else if (!a.used && !free_slot) free_slot = &a;
-    }
-    if (!slot) {
-        if (!free_slot) {
-            set_err("paged_decode: more than %d streams on one device", kArrivalStreams);
-            return nullptr;
-        }
-        slot = free_slot;
-        slot->used = true;
-        slot->stream = stream;
-    }
-    if (slot->count >= count) return slot->ptr;
-    if (slot->ptr) (void)hipFree(slot->ptr);  // waits for the device
-    slot->ptr = nullptr;
-    slot->count = 0;
-    const size_t n = count < 4096 ? 4096 : count;
-    if (hipMalloc(&slot->ptr, n * sizeof(uint32_t)) != hipSuccess) {
-        slot->ptr = nullptr;
-        set_err("paged_decode: cannot allocate %zu arrival counters", n);
-        return nullptr;
-    }
-    hipLaunchKernelGGL(fill_zero_u32, dim3((unsigned)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024)), dim3(256),
-                       0, stream, slot->ptr, n);
-    if (hipGetLastError() != hipSuccess) {
-        set_err("paged_decode: counter fill failed");
-        return nullptr;
-    }
-    slot->count = n;
-    return slot->ptr;
 }
 
 constexpr uint32_t kDefaultOldPermille = 700;
@@ -1161,7 +1103,7 @@ int vspec_rocm_kv_append_rope(const VspecPagedKV* kv, uint32_t batch, const int3
 }
 
 int vspec_rocm_kv_append_tokens(const VspecPagedKV* kv, uint32_t n_tokens, const int32_t* token_item,
-                                const int32_t* token_pos, const int32_t* block_tables,
+                                const int32_t* token_pos, const int32_t* block_tables, uint32_t n_items,
                                 uint32_t max_blocks_per_seq, const void* k_new, const void* v_new,
                                 int32_t src_dtype, void* stream) {
     if (!check_kv(kv, "kv_append_tokens")) return 0;
@@ -1170,14 +1112,15 @@ int vspec_rocm_kv_append_tokens(const VspecPagedKV* kv, uint32_t n_tokens, const
         return 0;
     }
     if (n_tokens == 0) return 1;
-    if (!token_item || !token_pos || !block_tables || !k_new || !v_new || max_blocks_per_seq == 0) {
-        set_err("kv_append_tokens: null argument");
+    if (!token_item || !token_pos || !block_tables || !k_new || !v_new || max_blocks_per_seq == 0 || n_items == 0) {
+        set_err("kv_append_tokens: null argument or no block-table rows");
         return 0;
     }
     AppendParams p = {};
     p.block_tables = block_tables;
     p.token_item = token_item;
     p.token_pos = token_pos;
+    p.n_items = n_items;
     p.k_new = (const uint8_t*)k_new;
     p.v_new = (const uint8_t*)v_new;
     p.batch = n_tokens;
@@ -1392,7 +1335,7 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.alpha = desc->clamp_alpha > 0.f ? desc->clamp_alpha : 4.5f;
     p.logit_clip = three ? 24.0f * kLog2e : INFINITY;
     p.input_clip = three ? 16.0f : INFINITY;
-    p.arrivals = nullptr;
+    p.split_grid = pl.split ? pl.grid_x : 0u;
     p.batch = desc->batch;
     p.max_tiles = pl.max_tiles;
     p.chunk_tiles = pl.chunk_tiles;
@@ -1434,8 +1377,6 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     if (pl.split) {
         // partial slots [grid][2][GW] of (max, sum) then of acc[D]
         p.part_acc = (float*)ws + (size_t)pl.grid_x * 2 * pl.gw * 2;
-        p.arrivals = arrival_counters((size_t)desc->batch * desc->kv.num_kv_heads * pl.gsplit, s);
-        if (!p.arrivals) return 0;
     }
     const dim3 grid = pl.split ? dim3(pl.grid_x) : dim3(pl.max_parts, desc->kv.num_kv_heads * pl.gsplit, desc->batch);
     int ok = 0;
@@ -1478,6 +1419,22 @@ int vspec_rocm_paged_decode_step(const VspecPagedAttnDesc* desc, const void* k_n
         return 0;
     }
     return paged_decode(desc, k_new, v_new, src_dtype);
+}
+
+int vspec_rocm_release_retired_workspaces(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_err("release_retired_workspaces: no current device");
+        return 0;
+    }
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    int ok = 1;
+    for (void* ptr : g_retired[dev]) {
+        if (hipFree(ptr) != hipSuccess) ok = 0;
+    }
+    g_retired[dev].clear();
+    if (!ok) set_err("release_retired_workspaces: hipFree failed");
+    return ok;
 }
 
 }  // extern "C"

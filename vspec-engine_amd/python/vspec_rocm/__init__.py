@@ -186,8 +186,9 @@ SIGNATURES = {
     "vspec_rocm_kv_gather_rows": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, _vp, _vp]),
     "vspec_rocm_paged_plan_step": (C.c_int, [_vp, C.POINTER(VspecRocmStepItem), C.c_size_t, _i32p_, C.c_size_t, _i32p_,
                                              _i32p_, _i32p_, _i32p_, C.c_size_t, C.POINTER(C.c_size_t)]),
-    "vspec_rocm_kv_append_tokens": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, C.c_uint32, _vp, _vp,
-                                              C.c_int32, _vp]),
+    "vspec_rocm_kv_append_tokens": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, C.c_uint32,
+                                              C.c_uint32, _vp, _vp, C.c_int32, _vp]),
+    "vspec_rocm_release_retired_workspaces": (C.c_int, []),
 }
 
 _LIB = None
@@ -226,11 +227,47 @@ def _ptr(t) -> int | None:
 
 
 def _stream(stream=None):
-    if stream is not None:
-        return stream
+    """The hipStream_t handle for the C-ABI: torch's current stream, a torch stream, or
+    a raw handle."""
     import torch
 
-    return torch.cuda.current_stream().cuda_stream
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return int(stream)
+
+
+def _foreign_stream(stream):
+    """The launch stream as a torch stream object when it is not torch's current stream
+    (temporaries made on the current stream must then be recorded on it), else None."""
+    import torch
+
+    if stream is None:
+        return None
+    s = stream if isinstance(stream, torch.cuda.Stream) else torch.cuda.ExternalStream(int(stream))
+    return None if s.cuda_stream == torch.cuda.current_stream().cuda_stream else s
+
+
+def _hold(stream, *tensors):
+    """Keep the caching allocator from handing the memory of these temporaries (made on
+    torch's current stream) to other work before the launch on `stream` has read them."""
+    s = _foreign_stream(stream)
+    if s is None:
+        return
+    for t in tensors:
+        if t is not None and getattr(t, "is_cuda", False):
+            t.record_stream(s)
+
+
+def _i32(t, device):
+    """An index tensor as contiguous int32 on the pool's device (the C-ABI reads int32)."""
+    import torch
+
+    out = torch.as_tensor(t).to(device=device, dtype=torch.int32).contiguous()
+    if out.device != torch.device(device):
+        raise VspecRocmError(f"index tensor on {out.device}, the pool is on {device}")
+    return out
 
 
 class PagedPool:
@@ -264,6 +301,10 @@ class PagedPool:
         else:
             self.ks = self.vs = self.kf = None
 
+    @property
+    def device(self):
+        return self.k.device
+
     def desc(self) -> VspecPagedKV:
         d = VspecPagedKV()
         d.dtype, d.num_blocks, d.block_tokens = self.dtype, self.num_blocks, self.block_tokens
@@ -282,11 +323,13 @@ def kv_append(pool: PagedPool, block_tables, start_pos, k_new, v_new, stream=Non
     B, n_new = k_new.shape[0], k_new.shape[1]
     src = KV_F32 if k_new.dtype == torch.float32 else KV_F16
     assert k_new.dtype in (torch.float32, torch.float16)
-    bt = block_tables.to(torch.int32).contiguous()
-    sp = start_pos.to(torch.int32).contiguous()
+    dev = pool.device
+    bt = _i32(block_tables, dev)
+    sp = _i32(start_pos, dev)
     d = pool.desc()
     _check(lib().vspec_rocm_kv_append(C.byref(d), B, bt.data_ptr(), bt.shape[1], sp.data_ptr(), n_new,
                                       k_new.data_ptr(), v_new.data_ptr(), src, _stream(stream)), "kv_append")
+    _hold(stream, bt, sp)
 
 
 def kv_append_rope(pool, block_tables, start_pos, k_new, v_new, rope_cos, rope_sin, rope_dim=None, q=None,
@@ -301,8 +344,9 @@ def kv_append_rope(pool, block_tables, start_pos, k_new, v_new, rope_cos, rope_s
     assert rope_cos.dtype == torch.float32 and rope_cos.is_contiguous() and rope_sin.is_contiguous()
     src = KV_F16 if k_new.dtype == torch.float16 else KV_F32
     rope_dim = int(rope_dim if rope_dim is not None else 2 * rope_cos.shape[1])
-    bt = block_tables.to(torch.int32).contiguous()
-    sp = start_pos.to(torch.int32).contiguous()
+    dev = pool.device
+    bt = _i32(block_tables, dev)
+    sp = _i32(start_pos, dev)
     q_out = None
     qin = qout = None
     hq = 0
@@ -315,6 +359,7 @@ def kv_append_rope(pool, block_tables, start_pos, k_new, v_new, rope_cos, rope_s
                                            k_new.data_ptr(), v_new.data_ptr(), src, rope_cos.data_ptr(),
                                            rope_sin.data_ptr(), rope_dim, rope_cos.shape[0], qin, qout, hq,
                                            _stream(stream)), "kv_append_rope")
+    _hold(stream, bt, sp, q_out)
     return q_out
 
 
@@ -328,27 +373,32 @@ def kv_append_tokens(pool, token_item, token_pos, block_tables, k_new, v_new, st
     if n == 0:
         return
     assert k_new.is_contiguous() and v_new.is_contiguous() and k_new.shape[0] == n
+    assert int(token_pos.numel()) == n
     src = KV_F16 if k_new.dtype == torch.float16 else KV_F32
-    bt = block_tables.to(torch.int32).contiguous()
+    dev = pool.device
+    ti = _i32(token_item, dev)
+    tp = _i32(token_pos, dev)
+    bt = _i32(block_tables, dev)
     kv = pool.desc()
-    _check(lib().vspec_rocm_kv_append_tokens(C.byref(kv), n, token_item.data_ptr(), token_pos.data_ptr(),
-                                             bt.data_ptr(), bt.shape[1], k_new.data_ptr(), v_new.data_ptr(), src,
+    _check(lib().vspec_rocm_kv_append_tokens(C.byref(kv), n, ti.data_ptr(), tp.data_ptr(), bt.data_ptr(),
+                                             bt.shape[0], bt.shape[1], k_new.data_ptr(), v_new.data_ptr(), src,
                                              _stream(stream)), "kv_append_tokens")
+    _hold(stream, ti, tp, bt)
 
 
 def kv_gather(pool: PagedPool, block_tables, ctx_lens, out_mode=GATHER_RAW, max_ctx_len=None, stream=None):
     """vspec_rocm_kv_gather -> (k, v, k_scales, v_scales) concatenated [T][H][D]."""
     import torch
 
-    bt = block_tables.to(torch.int32).contiguous()
-    cl = ctx_lens.to(torch.int32).contiguous()
+    dev = pool.device
+    bt = _i32(block_tables, dev)
+    cl = _i32(ctx_lens, dev)
     cl_host = cl.cpu()
     offs = torch.zeros(len(cl_host), dtype=torch.int64)
     if len(cl_host) > 1:
         offs[1:] = torch.cumsum(cl_host[:-1].to(torch.int64), 0)
     T = int(cl_host.sum())
     H, D = pool.num_kv_heads, pool.head_dim
-    dev = pool.k.device
     ks = vs = None
     if out_mode == GATHER_F32:
         ok = torch.zeros((T, H, D), dtype=torch.float32, device=dev)
@@ -367,16 +417,18 @@ def kv_gather(pool: PagedPool, block_tables, ctx_lens, out_mode=GATHER_RAW, max_
     _check(lib().vspec_rocm_kv_gather(C.byref(d), len(cl_host), bt.data_ptr(), bt.shape[1], cl.data_ptr(), mc,
                                       offs_d.data_ptr(), out_mode, ok.data_ptr(), ov.data_ptr(), _ptr(ks), _ptr(vs),
                                       _stream(stream)), "kv_gather")
+    _hold(stream, bt, cl, offs_d, ok, ov, ks, vs)
     return ok, ov, ks, vs
 
 
 def kv_compact(pool: PagedPool, src_blocks, dst_blocks, stream=None):
     import torch
 
-    s = src_blocks.to(torch.int32).contiguous()
-    t = dst_blocks.to(torch.int32).contiguous()
+    s = _i32(src_blocks, pool.device)
+    t = _i32(dst_blocks, pool.device)
     d = pool.desc()
     _check(lib().vspec_rocm_kv_compact(C.byref(d), len(s), s.data_ptr(), t.data_ptr(), _stream(stream)), "kv_compact")
+    _hold(stream, s, t)
 
 
 def make_decode_desc(pool: PagedPool, block_tables, ctx_lens, q, out, max_ctx_len, numerics=NUMERICS_PLAIN,
@@ -406,14 +458,15 @@ def paged_decode(pool: PagedPool, block_tables, ctx_lens, q, max_ctx_len=None, n
     import torch
 
     assert q.dtype == torch.float32 and q.is_contiguous()
-    bt = block_tables.to(torch.int32).contiguous()
-    cl = ctx_lens.to(torch.int32).contiguous()
+    bt = _i32(block_tables, pool.device)
+    cl = _i32(ctx_lens, pool.device)
     if max_ctx_len is None:
         max_ctx_len = int(cl.max().item()) if cl.numel() else 0
     if out is None:
         out = torch.empty_like(q)
     d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream)
     _check(lib().vspec_rocm_paged_decode_attention(C.byref(d)), "paged_decode_attention")
+    _hold(stream, bt, cl, out)
     return out
 
 
@@ -428,8 +481,8 @@ def paged_decode_step(pool: PagedPool, block_tables, ctx_lens, q, k_new, v_new, 
     assert k_new.is_contiguous() and v_new.is_contiguous() and k_new.shape == v_new.shape
     assert k_new.dtype in (torch.float32, torch.float16) and v_new.dtype == k_new.dtype
     src = KV_F32 if k_new.dtype == torch.float32 else KV_F16
-    bt = block_tables.to(torch.int32).contiguous()
-    cl = ctx_lens.to(torch.int32).contiguous()
+    bt = _i32(block_tables, pool.device)
+    cl = _i32(ctx_lens, pool.device)
     if max_ctx_len is None:
         max_ctx_len = int(cl.max().item()) if cl.numel() else 0
     if out is None:
@@ -437,6 +490,7 @@ def paged_decode_step(pool: PagedPool, block_tables, ctx_lens, q, k_new, v_new, 
     d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream)
     _check(lib().vspec_rocm_paged_decode_step(C.byref(d), k_new.data_ptr(), v_new.data_ptr(), src),
            "paged_decode_step")
+    _hold(stream, bt, cl, out)
     return out
 
 

@@ -26,9 +26,13 @@ class HandlePool:
     """A handle's device pool in the shape `paged_decode` expects (`desc()`)."""
 
     def __init__(self, kv: VspecPagedKV):
+        import torch
+
         self._kv = kv
         self.dtype, self.num_blocks, self.block_tokens = kv.dtype, kv.num_blocks, kv.block_tokens
         self.num_kv_heads, self.head_dim = kv.num_kv_heads, kv.head_dim
+        # handle pools live on the device that was current when the handle was created
+        self.device = torch.device("cuda", torch.cuda.current_device())
 
     def desc(self) -> VspecPagedKV:
         return self._kv
