@@ -148,6 +148,19 @@ int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc);
 int vspec_rocm_paged_decode_step(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
                                  int32_t src_dtype);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * vspec_rocm_paged_decode_step with its scratch (the partial states of work items split
+ * over several workgroups) in a fixed 6 MiB device array that the library holds per GPU
+ * for the life of the process; desc->workspace is ignored and nothing is allocated or
+ * freed.  A plan whose partial states need more (vspec_rocm_paged_decode_workspace_bytes
+ * above 6 MiB: chunked partitions of long batches, f32 pools split into many
+ * partitions) is rejected with an error before any launch.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams, other host threads)
+ * race and must be serialised by the caller. */
+int vspec_rocm_paged_decode_step_noalloc(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
+                                         int32_t src_dtype);
+
 /* Free the library workspaces that later, larger decodes replaced on the current device.
  * They are kept until this call because a captured HIP graph may still use them; call it
  * only when no such graph will be replayed again. */

@@ -739,6 +739,31 @@ void* library_workspace(size_t bytes) {
     return w.ptr;
 }
 
+// ---- the no-allocation decode step's device scratch ----
+// Partial states of vspec_rocm_paged_decode_step_noalloc live in this file-scope array,
+// one copy per device for the life of the process.  Host code never uses its name as an
+// address: the per-device address comes from hipGetSymbolAddress on the entry point's
+// first call on that device.
+constexpr size_t kScratchBytes = (size_t)6 << 20;  // partial (max, sum, acc) slots
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+void* g_scratch_ptr[64];
+bool g_scratch_ready[64];
+
+uint8_t* scratch_address(int dev) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (!g_scratch_ready[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_err("paged_decode_step_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+        g_scratch_ready[dev] = true;
+    }
+    return (uint8_t*)g_scratch_ptr[dev];
+}
+
 constexpr uint32_t kDefaultOldPermille = 700;
 
 // workgroups per CU of the balanced MFMA split: VSPEC_ROCM_DECODE_WGS_PER_CU (1..8) when
@@ -1268,7 +1293,10 @@ namespace {
 
 // Decode attention, with the decode step's append of k_new / v_new first when they are
 // given (one launch for the f16 and int4 kernels, an append launch before the f32 one).
-int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new, int32_t src_dtype) {
+// noalloc: the partial states come from the file-scope scratch array
+// (no allocation, no library state beyond it); the descriptor's workspace is ignored.
+int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new, int32_t src_dtype,
+                 bool noalloc) {
     if (!desc) {
         set_err("paged_decode: null descriptor");
         return 0;
@@ -1290,7 +1318,22 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     DecodePlan pl;
     if (!plan_decode(desc, &pl)) return 0;
     void* ws = nullptr;
-    if (pl.ws_bytes) {
+    if (noalloc) {
+        if (pl.ws_bytes > kScratchBytes) {
+            set_err("paged_decode_step_noalloc: the plan needs %zu bytes of partial states, more than the "
+                    "%zu-byte scratch (use vspec_rocm_paged_decode_step with a workspace)",
+                    pl.ws_bytes, kScratchBytes);
+            return 0;
+        }
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+            set_err("paged_decode_step_noalloc: no current device");
+            return 0;
+        }
+        uint8_t* base = scratch_address(dev);
+        if (!base) return 0;
+        ws = pl.ws_bytes ? base : nullptr;
+    } else if (pl.ws_bytes) {
         if (desc->workspace) {
             if (desc->workspace_bytes < pl.ws_bytes) {
                 set_err("paged_decode: workspace too small (%zu < %zu)", desc->workspace_bytes, pl.ws_bytes);
@@ -1404,21 +1447,31 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
 extern "C" {
 
 int vspec_rocm_paged_decode_attention(const VspecPagedAttnDesc* desc) {
-    return paged_decode(desc, nullptr, nullptr, VSPEC_KV_F32);
+    return paged_decode(desc, nullptr, nullptr, VSPEC_KV_F32, false);
+}
+
+static int decode_step(const char* who, const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
+                       int32_t src_dtype, bool noalloc) {
+    const bool empty = desc && desc->batch == 0;  // a no-op, like every other entry point
+    if (!empty && (!k_new || !v_new)) {
+        set_err("%s: null k_new or v_new", who);
+        return 0;
+    }
+    if (src_dtype != VSPEC_KV_F32 && src_dtype != VSPEC_KV_F16) {
+        set_err("%s: src_dtype must be f32 or f16", who);
+        return 0;
+    }
+    return paged_decode(desc, k_new, v_new, src_dtype, noalloc);
 }
 
 int vspec_rocm_paged_decode_step(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
                                  int32_t src_dtype) {
-    const bool empty = desc && desc->batch == 0;  // a no-op, like every other entry point
-    if (!empty && (!k_new || !v_new)) {
-        set_err("paged_decode_step: null k_new or v_new");
-        return 0;
-    }
-    if (src_dtype != VSPEC_KV_F32 && src_dtype != VSPEC_KV_F16) {
-        set_err("paged_decode_step: src_dtype must be f32 or f16");
-        return 0;
-    }
-    return paged_decode(desc, k_new, v_new, src_dtype);
+    return decode_step("paged_decode_step", desc, k_new, v_new, src_dtype, false);
+}
+
+int vspec_rocm_paged_decode_step_noalloc(const VspecPagedAttnDesc* desc, const void* k_new, const void* v_new,
+                                         int32_t src_dtype) {
+    return decode_step("paged_decode_step_noalloc", desc, k_new, v_new, src_dtype, true);
 }
 
 int vspec_rocm_release_retired_workspaces(void) {

@@ -156,6 +156,7 @@ SIGNATURES = {
     "vspec_rocm_paged_decode_workspace_bytes": (C.c_size_t, [C.POINTER(VspecPagedAttnDesc)]),
     "vspec_rocm_paged_decode_attention": (C.c_int, [C.POINTER(VspecPagedAttnDesc)]),
     "vspec_rocm_paged_decode_step": (C.c_int, [C.POINTER(VspecPagedAttnDesc), _vp, _vp, C.c_int32]),
+    "vspec_rocm_paged_decode_step_noalloc": (C.c_int, [C.POINTER(VspecPagedAttnDesc), _vp, _vp, C.c_int32]),
     "vspec_rocm_sync": (C.c_int, [_vp]),
     "vspec_rocm_last_error": (C.c_char_p, []),
     "vspec_rocm_device_count": (C.c_int, []),
