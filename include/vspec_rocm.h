@@ -131,6 +131,15 @@ typedef struct VspecPagedAttnDesc {
     void* workspace;                 /* device scratch (no init needed) or NULL: library's */
     size_t workspace_bytes;
     void* stream;                    /* hipStream_t or NULL */
+    /* Optional, device int32 [batch][max_blocks_per_seq], or NULL: tokens held by the
+     * block of each table entry, slots 0 .. used-1 (reference page_meta.used_tokens,
+     * kv_paged_cache.c:335-347).  Prefix reuse leaves partly filled blocks in the middle
+     * of a session (kv_paged_cache.c:223-234, 276); with block_used set, ctx_lens[b] is
+     * the sequence's span in table-slot space -- entry i covers positions [i*P, (i+1)*P),
+     * span = (last entry) * P + its used count -- and positions at or above their block's
+     * used count are skipped.  The decode step appends at span - 1.  NULL: every block is
+     * full except the last, and ctx_lens[b] is the token count. */
+    const int32_t* block_used;
 } VspecPagedAttnDesc;
 
 size_t vspec_rocm_paged_decode_workspace_bytes(const VspecPagedAttnDesc* desc);

@@ -68,9 +68,16 @@ int vspec_rocm_paged_page_info(const VspecRocmPagedMeta* m, size_t page, uint32_
                                uint32_t* used_tokens, uint32_t* ref_count);
 /* Block table for the decode kernel: pages in order when every page but the last is
  * full (then *ctx_len = session tokens); returns 0 otherwise (prefix reuse left a
- * partly filled page in the middle: gather rows instead). */
+ * partly filled page in the middle: use vspec_rocm_paged_block_layout). */
 int vspec_rocm_paged_block_table(const VspecRocmPagedMeta* m, uint64_t session_id, int32_t* out,
                                  size_t cap, uint32_t* ctx_len);
+/* Any session as the decode kernel's (block table, block_used, span): blocks[i] = the
+ * i-th page, used[i] = its used tokens (the counts get_token_ptr walks,
+ * kv_paged_cache.c:335-347), *span = (pages - 1) * page_tokens + last page's used count
+ * (the ctx_lens entry when VspecPagedAttnDesc.block_used is set), *tokens = the
+ * session's token count.  Returns 0 for an unknown session or cap < pages. */
+int vspec_rocm_paged_block_layout(const VspecRocmPagedMeta* m, uint64_t session_id, int32_t* blocks,
+                                  int32_t* used, size_t cap, uint32_t* span, uint32_t* tokens);
 
 /* A continuous-batching work item: same fields and layout as VspecContinuousBatchItem
  * (continuous_batch.h:15-20).  request_id doubles as the paged-cache session id;
@@ -87,14 +94,19 @@ typedef struct VspecRocmStepItem {
  * context after the step (ctx_lens[i]) and the position of its first new token
  * (start_pos[i]); and, per packed new token t (items in order, quota tokens each), its
  * item (token_item[t]) and position (token_pos[t]) -- the inputs of
- * vspec_rocm_kv_append_tokens and of the decode descriptor.  Returns 0 on a repeated
- * request, a failed reservation, an eviction of an earlier item's session by a later
- * one, a session that is not a block table (shared partly filled middle page), or
- * outputs that are too small; reservations made before the failure stay made. */
+ * vspec_rocm_kv_append_tokens and of the decode descriptor.  Positions are in
+ * table-slot space (page index * page_tokens + slot), the token index while every page
+ * but the last is full.  block_used (optional, [n_items][max_blocks]) receives each
+ * entry's used count, and ctx_lens the span (see VspecPagedAttnDesc.block_used): every
+ * session can then be decoded, partly filled middle pages included.  Without it a
+ * session with such a page fails the step.  Returns 0 on a repeated request, a failed
+ * reservation, an eviction of an earlier item's session by a later one, or outputs that
+ * are too small; reservations made before the failure stay made. */
 int vspec_rocm_paged_plan_step(VspecRocmPagedMeta* m, const VspecRocmStepItem* items,
-                               size_t n_items, int32_t* block_tables, size_t max_blocks,
-                               int32_t* ctx_lens, int32_t* start_pos, int32_t* token_item,
-                               int32_t* token_pos, size_t max_tokens, size_t* n_tokens);
+                               size_t n_items, int32_t* block_tables, int32_t* block_used,
+                               size_t max_blocks, int32_t* ctx_lens, int32_t* start_pos,
+                               int32_t* token_item, int32_t* token_pos, size_t max_tokens,
+                               size_t* n_tokens);
 
 /* Append packed new tokens (device pointers): token t of k_new/v_new ([n][H][D] in
  * src_dtype) goes to position token_pos[t] of the sequence whose block table is row

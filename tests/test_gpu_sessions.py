@@ -145,6 +145,8 @@ def test_decode_over_handle_pool(ref, gpu, mode):
         assert cache.reuse_prefix(7, 1, 0)
         cache.append(rng.standard_normal((H, D)), rng.standard_normal((H, D)), session_id=7)
         assert cache.session_tokens(7) == 174
+        # a plain block table cannot express session 7 (its shared page with 13 tokens sits
+        # in the middle); the layout with per-block used counts can
         assert cache.block_table(7, 32) is None
         sids = [1, 2, 3, 4, 5]
         tabs, ctx = [], []
@@ -153,17 +155,30 @@ def test_decode_over_handle_pool(ref, gpu, mode):
             tabs.append(t)
             ctx.append(n)
         assert ctx == [173, 64, 300, 1, 117]
-        q = rng.standard_normal((len(sids), Hq, D)).astype(np.float32)
+        q = rng.standard_normal((len(sids) + 1, Hq, D)).astype(np.float32)
         pool = cache.device_pool()
         out = vr.paged_decode(pool, torch.from_numpy(np.stack(tabs)).to(gpu),
-                              torch.tensor(ctx, dtype=torch.int32, device=gpu), torch.from_numpy(q).to(gpu),
-                              numerics=mode)
+                              torch.tensor(ctx, dtype=torch.int32, device=gpu),
+                              torch.from_numpy(q[: len(sids)]).to(gpu), numerics=mode)
         got = out.cpu().numpy()
         for i, s in enumerate(sids):
             k, v = cache.read_tokens(session_id=s)
             want = ref.attention_gqa(mode, q[i], k, v)
             err = float(np.abs(got[i] - want).max())
-            assert err <= 1e-4, (s, err)
+            assert err <= 2e-5, (s, err)
+        # every session through block layouts, session 7 included
+        lay = [cache.block_layout(s, 32) for s in sids + [7]]
+        assert lay[-1][3] == 174 and lay[-1][2] == 11 * 16 + 1 and (lay[-1][1][:11] < 16).any()
+        out = vr.paged_decode(pool, torch.from_numpy(np.stack([l[0] for l in lay])).to(gpu),
+                              torch.tensor([l[2] for l in lay], dtype=torch.int32, device=gpu),
+                              torch.from_numpy(q).to(gpu), numerics=mode,
+                              block_used=torch.from_numpy(np.stack([l[1] for l in lay])).to(gpu))
+        got = out.cpu().numpy()
+        for i, s in enumerate(sids + [7]):
+            k, v = cache.read_tokens(session_id=s)
+            want = ref.attention_gqa(mode, q[i], k, v)
+            err = float(np.abs(got[i] - want).max())
+            assert err <= 2e-5, (s, err)
     finally:
         cache.close()
 
@@ -217,3 +232,139 @@ def test_continuous_batching_steps(oracle, ref, gpu, dtype):
         say(f"[cb] dtype={dtype} steps={si + 1}")
     finally:
         vr.lib().vspec_rocm_paged_meta_destroy(m)
+
+
+def _pool_rows(lib, pool, tab, used, P, dev):
+    """A session's rows [n][Hkv][D] as f32 through the row gather, in the order the
+    reference's get_token_ptr walk visits them (entry by entry, used slots each)."""
+    import ctypes as C
+    import torch
+
+    pos = [e * P + s for e in range(len(used)) if tab[e] >= 0 for s in range(int(used[e]))]
+    pages = torch.tensor([int(tab[p // P]) for p in pos], dtype=torch.int32, device=dev)
+    slots = torch.tensor([p % P for p in pos], dtype=torch.int32, device=dev)
+    n = len(pos)
+    ok = torch.empty((n, pool.num_kv_heads, pool.head_dim), dtype=torch.float32, device=dev)
+    ov = torch.empty_like(ok)
+    d = pool.desc()
+    assert lib.vspec_rocm_kv_gather_rows(C.byref(d), n, pages.data_ptr(), slots.data_ptr(), ok.data_ptr(),
+                                         ov.data_ptr(), None) == 1
+    torch.cuda.synchronize()
+    return ok.cpu().numpy(), ov.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2])  # f32, f16, int4 pools
+def test_partial_middle_pages_decode(oracle, ref, gpu, dtype):
+    """Prefix reuse of a partly filled page (kv_paged_cache.c:223-234) leaves it in the
+    middle of the target and, once the source appends again (a new page: :276), of the
+    source.  Steps planned with block_used append through kv_append_tokens at slot-space
+    positions, with the reference paged cache appending the same tokens; every session
+    then decodes in one batch (block tables, used counts, spans), and a fused decode step
+    appends one more token to each.  The pool rows equal the reference cache's walk bit
+    for bit (f32, and f16 as its exact f32 values) and the outputs match attention_ref
+    over the reference's gathered rows (int4: over the pool's dequantised rows)."""
+    import torch
+    import vspec_rocm as vr
+    from vspec_rocm.sessions import plan_step
+
+    P, MAXP, Hkv, Hq, D, MB = 16, 160, 2, 8, 128, 16
+    L = vr.lib()
+    m = L.vspec_rocm_paged_meta_create(P, MAXP, 0, 0)
+    pool = vr.PagedPool(dtype, MAXP, P, Hkv, D, device=gpu)
+    c = ref.lib.vr_paged_new(P, MAXP, Hkv, D)
+    rng = np.random.default_rng(40 + dtype)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+    def tokens(n):
+        k = rng.standard_normal((n, Hkv, D)).astype(np.float32)
+        v = rng.standard_normal((n, Hkv, D)).astype(np.float32)
+        if dtype == 0:
+            return k, v, dev(k), dev(v)
+        k16, v16 = oracle.f32_to_f16(k), oracle.f32_to_f16(v)
+        to16 = lambda h: torch.from_numpy(h.view(np.int16).copy()).view(torch.float16).to(gpu)
+        return oracle.f16_to_f32(k16), oracle.f16_to_f32(v16), to16(k16), to16(v16)
+
+    def run(items):
+        plan = plan_step(m, items, max_blocks=MB, with_used=True)
+        n = plan["token_item"].size
+        kf, vf, kd, vd = tokens(n)
+        for t in range(n):
+            sid = items[int(plan["token_item"][t])][0]
+            assert ref.lib.vspec_kv_paged_append(c, sid, kf[t].ctypes.data_as(_f32p), vf[t].ctypes.data_as(_f32p))
+        vr.kv_append_tokens(pool, dev(plan["token_item"]), dev(plan["token_pos"]), dev(plan["block_tables"]), kd, vd)
+        return plan
+
+    def reuse(t, s_, mt):
+        assert L.vspec_rocm_paged_reuse_prefix(m, t, s_, mt) == ref.lib.vspec_kv_paged_reuse_prefix(c, t, s_, mt) == 1
+
+    def layouts(sids):
+        tabs, used, spans = [], [], []
+        for s_ in sids:
+            tb = np.full(MB, -1, np.int32)
+            us = np.zeros(MB, np.int32)
+            sp, nt = C.c_uint32(), C.c_uint32()
+            assert L.vspec_rocm_paged_block_layout(m, s_, tb.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                   us.ctypes.data_as(C.POINTER(C.c_int32)), MB, C.byref(sp),
+                                                   C.byref(nt))
+            assert nt.value == ref.lib.vspec_kv_paged_session_tokens(c, s_)
+            tabs.append(tb)
+            used.append(us)
+            spans.append(sp.value)
+        return np.stack(tabs), np.stack(used), np.array(spans, np.int32)
+
+    def expected(mode, sids, tabs, used, q):
+        out, vmax = [], 0.0
+        for i, s_ in enumerate(sids):
+            n = ref.lib.vspec_kv_paged_session_tokens(c, s_)
+            rk = np.zeros((n, Hkv, D), np.float32)
+            rv = np.zeros_like(rk)
+            assert ref.lib.vr_paged_read(c, s_, rk.ctypes.data_as(_f32p), rv.ctypes.data_as(_f32p), 0) == n
+            gk, gv = _pool_rows(L, pool, tabs[i], used[i], P, gpu)
+            if dtype != 2:
+                # the pool holds exactly the reference cache's values, in its walk order
+                assert np.array_equal(gk, rk) and np.array_equal(gv, rv), s_
+                k, v = rk, rv
+            else:
+                k, v = gk, gv
+            vmax = max(vmax, float(np.abs(v).max()))
+            out.append(ref.attention_gqa(mode, q[i], k, v))
+        tol = 2e-5 if dtype != 2 else min(4e-3, 2.5e-4 * vmax + 2e-5)
+        return np.stack(out), tol
+
+    try:
+        say(f"[partial pages] dtype={dtype}")
+        run([(1, 1, 37, 0)])                           # 2 full pages + 5 tokens
+        run([(2, 1, 16, 0), (3, 1, 50, 0)])
+        reuse(5, 1, 0)                                 # shares 1's partly filled page
+        reuse(6, 3, 40)                                # two whole pages (32 tokens)
+        run([(5, 1, 20, 0), (1, 1, 7, 0), (6, 1, 3, 0)])   # 5 and 1 open pages after it
+        reuse(7, 5, 0)
+        run([(7, 1, 3, 0), (2, 1, 1, 0)])
+        sids = [1, 2, 3, 5, 6, 7]
+        tabs, used, spans = layouts(sids)
+        npages = (tabs >= 0).sum(1)
+        assert any((used[i, : npages[i] - 1] < P).any() for i in range(len(sids)))  # partial middle pages
+        q = rng.standard_normal((len(sids), Hq, D)).astype(np.float32)
+        for mode in (1, 0):
+            got = vr.paged_decode(pool, dev(tabs), dev(spans), dev(q), numerics=mode, block_used=dev(used)).cpu().numpy()
+            want, tol = expected(mode, sids, tabs, used, q)
+            err = float(np.abs(got - want).max())
+            say(f"    decode mode={mode} max-abs {err:.2e} (bound {tol:.1e})")
+            assert err <= tol
+        # fused decode step: one new token per session at its span (planned with block_used)
+        plan = plan_step(m, [(s_, 2, 1, 0) for s_ in sids], max_blocks=MB, with_used=True)
+        assert (plan["token_pos"] == plan["ctx_lens"] - 1).all()
+        kf, vf, kd, vd = tokens(len(sids))
+        for i, s_ in enumerate(sids):
+            assert ref.lib.vspec_kv_paged_append(c, s_, kf[i].ctypes.data_as(_f32p), vf[i].ctypes.data_as(_f32p))
+        got = vr.paged_decode_step(pool, dev(plan["block_tables"]), dev(plan["ctx_lens"]), dev(q), kd, vd,
+                                   numerics=1, block_used=dev(plan["block_used"])).cpu().numpy()
+        tabs2, used2, spans2 = layouts(sids)
+        assert (tabs2 == plan["block_tables"]).all() and (used2 == plan["block_used"]).all()
+        want, tol = expected(1, sids, tabs2, used2, q)
+        err = float(np.abs(got - want).max())
+        say(f"    decode step max-abs {err:.2e} (bound {tol:.1e})")
+        assert err <= tol
+    finally:
+        L.vspec_rocm_paged_meta_destroy(m)
+        ref.lib.vr_paged_free(c)

@@ -230,6 +230,74 @@ def test_plan_step_follows_reference_scheduler(lib, ref, seed):
         ref.lib.vr_paged_free(c)
 
 
+def _slot_space(used, P):
+    """Table-slot positions of a session's tokens in order: entry e holds used[e] tokens
+    at positions e*P .. e*P + used[e] - 1 (the get_token_ptr walk, kv_paged_cache.c:335-347)."""
+    return [e * P + s for e in range(len(used)) for s in range(int(used[e]))]
+
+
+def test_plan_step_partial_middle_pages(lib, ref):
+    """Prefix reuse that shares a partly filled page leaves it in the middle of both the
+    target and, once the source appends again, the source (kv_paged_cache.c:223-234, 276).
+    With block_used the planner still expresses every session: the used counts equal the
+    reference pages', the span is the slot-space end, every token maps through the table
+    to the (page, slot) the reference cache holds it in, and the new tokens' positions land
+    where the reference appends them."""
+    from vspec_rocm.sessions import plan_step
+
+    P, MAXP, H, D = 4, 64, 1, 8
+    m = lib.vspec_rocm_paged_meta_create(P, MAXP, 0, 0)
+    c = ref.lib.vr_paged_new(P, MAXP, H, D)
+    tok = np.zeros(H * D, np.float32)
+    app = lambda sid: ref.lib.vspec_kv_paged_append(c, sid, tok.ctypes.data_as(_f32p), tok.ctypes.data_as(_f32p))
+    steps = [
+        ("plan", [(1, 1, 6, 0)]),                          # 1: a full page + 2 tokens
+        ("reuse", (2, 1, 0)),                              # 2 shares both, the partial one too
+        ("plan", [(1, 2, 3, 0), (2, 2, 2, 0), (3, 1, 5, 0)]),  # 1 and 2 open new pages
+        ("reuse", (4, 2, 0)),                              # 4 shares 2's partial middle page
+        ("plan", [(4, 2, 1, 0), (2, 2, 7, 0), (1, 2, 1, 0)]),
+        ("reuse", (5, 3, 3)),                              # max_tokens 3 < the first page: none
+        ("plan", [(5, 1, 9, 0), (4, 2, 4, 0)]),
+    ]
+    try:
+        saw_partial_middle = False
+        for kind, arg in steps:
+            if kind == "reuse":
+                assert lib.vspec_rocm_paged_reuse_prefix(m, *arg) == ref.lib.vspec_kv_paged_reuse_prefix(c, *arg)
+                continue
+            before = [ref.lib.vspec_kv_paged_session_tokens(c, it[0]) for it in arg]
+            plan = plan_step(m, arg, max_blocks=16, with_used=True)
+            for it in arg:
+                for _ in range(it[2]):
+                    assert app(it[0])
+            off = 0
+            for i, it in enumerate(arg):
+                sid, q = it[0], it[2]
+                tab, used, span = plan["block_tables"][i], plan["block_used"][i], int(plan["ctx_lens"][i])
+                n = ref.lib.vspec_kv_paged_session_tokens(c, sid)
+                assert n == before[i] + q == int(used.sum())
+                npages = int((tab >= 0).sum())
+                assert (tab[:npages] >= 0).all() and (tab[npages:] == -1).all()
+                assert span == ((npages - 1) * P + int(used[npages - 1]) if npages else 0)
+                saw_partial_middle |= bool((used[: max(npages - 1, 0)] < P).any())
+                for e in range(npages):
+                    alloc, u, rc = C.c_uint32(), C.c_uint32(), C.c_uint32()
+                    ref.lib.vr_paged_page_meta(c, int(tab[e]), C.byref(alloc), C.byref(u), C.byref(rc))
+                    assert u.value == used[e], (sid, e)
+                pos = _slot_space(used[:npages], P)
+                assert len(pos) == n
+                for t in range(n):
+                    assert _ref_locate(ref, c, P, H, D, sid, t) == (int(tab[pos[t] // P]), pos[t] % P), (sid, t)
+                # the packed new tokens are the session's last q, at their slot-space positions
+                assert list(plan["token_pos"][off:off + q]) == pos[n - q:]
+                assert q == 0 or plan["start_pos"][i] == pos[n - q]
+                off += q
+        assert saw_partial_middle
+    finally:
+        lib.vspec_rocm_paged_meta_destroy(m)
+        ref.lib.vr_paged_free(c)
+
+
 def test_plan_step_rejects_bad_steps(lib):
     from vspec_rocm import VspecRocmError
     from vspec_rocm.sessions import plan_step

@@ -36,7 +36,7 @@ struct Frags {
 };
 
 // PB: block_tokens known at compile time (16), or 0 for any multiple of 16;
-// NB: tiles in flight per wave
+// NB: tiles in flight per wave; USED: per-block used counts cap each tile (block_used)
 //
 // Schedule: the workgroup takes the tile range [lo, hi) of the work split (it may start
 // and end inside work items and span several); wave w streams the range's tiles
@@ -46,7 +46,7 @@ struct Frags {
 // old one to an LDS merge slot, resets it and prepares the new item's q operands from
 // q rows staged in LDS up front.  The last of the four waves to hand in an item's state
 // merges the four; no barrier stops the ring.
-template <int D, int GW, int PB, int NB>
+template <int D, int GW, int PB, int NB, bool USED>
 __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     constexpr int NQK = D / 32;   // QK MFMAs per tile (each on 32 d)
     constexpr int NDT = D / 16;   // PV d-tiles
@@ -135,19 +135,20 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const int ctx_cap = (int)(p.max_blocks * p.block_tokens);
 
     // Loads are issued unconditionally (a tile past the range or behind an invalid
-    // table entry reads block 0 and reports false): with no branches around them the
-    // compiler counts outstanding loads exactly and waits only for the tile it needs.
-    // `lc` is the work item of the tiles being loaded (it runs NB tiles ahead).
+    // table entry reads block 0 and holds no valid token): with no branches around them
+    // the compiler counts outstanding loads exactly and waits only for the tile it needs.
+    // `lc` is the work item of the tiles being loaded (it runs NB tiles ahead).  Returns
+    // how many of the tile's tokens its block holds (16, or block_used's cap; 0: none).
     ItemCursor lc = first;
-    auto load = [&](int t, Frags<D>& f) -> bool {
+    auto load = [&](int t, Frags<D>& f) -> int {
         t = __builtin_amdgcn_readfirstlane(t);
         const bool in_range = t < ws.hi;
         if (in_range) {
             while (t >= lc.item0 + lc.U) cursor_next(p, ips, lc);
         }
         const int tile = in_range ? t - lc.item0 : 0;
-        const const_i32* table = as_const(p.block_tables) + (size_t)lc.b * p.max_blocks;
-        const int entry = table[tile / tiles_per_block];
+        const size_t row = (size_t)lc.b * p.max_blocks + tile / tiles_per_block;
+        const int entry = as_const(p.block_tables)[row];
         const bool ok = in_range && entry >= 0 && (uint32_t)entry < p.num_blocks;
         const size_t tidx = (size_t)(ok ? entry : 0) * p.hkv + lc.y / (int)p.gsplit;
         const int slot0 = (tile % tiles_per_block) * kTile;
@@ -157,7 +158,8 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         const _Float16* vt = vbase + tidx * (size_t)D * P + slot0 + 4 * g;
 #pragma unroll
         for (int j = 0; j < NDT; ++j) f.v[j] = load_stream2(vt + (size_t)(16 * j + n) * P);
-        return ok;
+        if constexpr (USED) return ok ? used_cap(as_const(p.block_used)[row], slot0) : 0;
+        return ok ? kTile : 0;
     };
 
     f4_t acc[NDT];
@@ -285,10 +287,10 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         }
     };
 
-    // one tile; a tile that is out of range or behind an invalid table entry has no
-    // valid keys and contributes nothing
-    auto process = [&](Frags<D>& f, const bool ok, const int tile, const int ctx) {
-        const int nvalid = ok ? min(kTile, ctx - tile * kTile) : 0;
+    // one tile holding `cap` valid tokens (slots 0 .. cap-1 of its block; 0 for a tile
+    // out of range or behind an invalid table entry, which contributes nothing)
+    auto process = [&](Frags<D>& f, const int cap, const int tile, const int ctx) {
+        const int nvalid = max(0, min(cap, ctx - tile * kTile));
         const Screen sn = screen(f, nvalid);
         f4_t sc = qk(f);
         const uint32_t flagged = tokens(__builtin_amdgcn_ballot_w64(sn.flag));
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const int t0 = ws.lo + wave;
     const int nt = wave < len ? (len - wave + kWaves - 1) / kWaves : 0;
     Frags<D> f[NB];
-    bool ok[NB];
+    int ok[NB];
     // the first tiles' loads go out before the q rows are staged, so that the two
     // latencies overlap (the barrier below does not wait for them)
 #pragma unroll
@@ -440,14 +442,20 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
 #define VSPEC_F16_TILES_IN_FLIGHT 2
 #endif
 
-template <int D, int GW>
-void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
+template <int D, int GW, bool USED>
+void launch_used(const DecodeParams& p, dim3 grid, hipStream_t s) {
     constexpr int NB = VSPEC_F16_TILES_IN_FLIGHT;
     if (p.block_tokens == 16) {
-        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 16, NB>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 16, NB, USED>), grid, dim3(256), 0, s, p);
     } else {
-        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0, NB>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0, NB, USED>), grid, dim3(256), 0, s, p);
     }
+}
+
+template <int D, int GW>
+void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
+    if (p.block_used) launch_used<D, GW, true>(p, grid, s);
+    else launch_used<D, GW, false>(p, grid, s);
     // items split over several workgroups (same split: the f16 kernel's pair shares)
     const dim3 merge_grid(p.batch * p.hkv * p.gsplit);
     hipLaunchKernelGGL((decode_merge_split<D, GW, true>), merge_grid, dim3(kWaves * 64), 0, s, p);

@@ -74,7 +74,8 @@ __device__ __forceinline__ _Float16 half_at(const uint32_t* w, int i) {
 
 // FL: the tile loop takes the pool's clamp flags (and screens only what they cannot say);
 // without FL it screens every tile, a lighter loop for short per-workgroup shares.
-template <int D, int GW, int PB, int NB, bool FL>
+// USED: per-block used counts cap each tile (block_used).
+template <int D, int GW, int PB, int NB, bool FL, bool USED>
 __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(DecodeParams p) {
     constexpr int NQ = D / 32;   // code dwords per lane = QK MFMAs per tile = groups
     constexpr int NG = D / 32;
@@ -176,6 +177,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         const int P = PB ? PB : (int)p.block_tokens;
         const int tiles_per_block = P / kTile;
         const const_i32* table = as_const(p.block_tables) + (size_t)b * p.max_blocks;
+        const const_i32* used_row = USED ? as_const(p.block_used) + (size_t)b * p.max_blocks : nullptr;
         const int own_group = (g * NQ) >> 2;
         const int col_group = (n >> 2) % NG;
 
@@ -186,13 +188,16 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         auto valid_mask = [](int nvalid) -> uint32_t { return nvalid >= kTile ? 0xffffu : (1u << nvalid) - 1u; };
 
         // Loads are issued unconditionally (a tile past the range or behind an invalid
-        // table entry reads block 0 and reports false): with no branches around them the
-        // compiler counts outstanding loads exactly and waits only for the tile it needs.
-        // The tile index is wave-uniform, so the table read stays on the scalar unit.
-        auto load = [&](int tile, I4Frags<D>& f) -> bool {
+        // table entry reads block 0 and holds no valid token): with no branches around
+        // them the compiler counts outstanding loads exactly and waits only for the tile
+        // it needs.  The tile index is wave-uniform, so the table read stays on the scalar
+        // unit.  Returns how many of the tile's tokens its block holds (16, or
+        // block_used's cap; 0: none).
+        auto load = [&](int tile, I4Frags<D>& f) -> int {
             tile = __builtin_amdgcn_readfirstlane(tile);
             const bool in_range = tile < tile_end;
-            const int entry = table[(in_range ? tile : tile_end - 1) / tiles_per_block];
+            const int entry_idx = (in_range ? tile : tile_end - 1) / tiles_per_block;
+            const int entry = table[entry_idx];
             const bool ok = in_range && entry >= 0 && (uint32_t)entry < p.num_blocks;
             const int phys = ok ? entry : 0;
             const size_t bh = (size_t)phys * p.hkv + hk;
@@ -222,7 +227,8 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 const uint4 w = load_stream4(vs + i);
                 f.vs[4 * i] = w.x; f.vs[4 * i + 1] = w.y; f.vs[4 * i + 2] = w.z; f.vs[4 * i + 3] = w.w;
             }
-            return ok;
+            if constexpr (USED) return ok ? used_cap(used_row[entry_idx], slot0) : 0;
+            return ok ? kTile : 0;
         };
 
         // score clip per lane: columns that hold no head clip to -inf (3-bit mode: +-24*log2e)
@@ -353,9 +359,9 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 
         // Two tiles per step: k-slot 8g + i of the PV MFMA is token 4g + i of tile A (i < 4)
         // or token 4g + i - 4 of tile B.
-        auto process = [&](I4Frags<D>& fa, I4Frags<D>& fb, const bool oka, const bool okb, const int tile_a) {
-            const int nva = oka ? min(kTile, ctx - tile_a * kTile) : 0;
-            const int nvb = okb ? min(kTile, ctx - (tile_a + 1) * kTile) : 0;
+        auto process = [&](I4Frags<D>& fa, I4Frags<D>& fb, const int capa, const int capb, const int tile_a) {
+            const int nva = max(0, min(capa, ctx - tile_a * kTile));
+            const int nvb = max(0, min(capb, ctx - (tile_a + 1) * kTile));
             // clamp flags: from the pool, or from the screen (both tiles in one basic block:
             // their chains interleave)
             // the tile this launch appended into: its word with the appended key's flag
@@ -449,7 +455,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // Pairs of consecutive tiles; NB pairs in flight per wave.  Pair i (from the
         // partition start) is tiles tile_begin + 2i, +1; wave w takes i = w, w + kWaves, ...
         I4Frags<D> fa[NB], fb[NB];
-        bool oka[NB], okb[NB];
+        int oka[NB], okb[NB];
         const int step = 2 * kWaves;
         const int t0 = tile_begin + 2 * wave;
 #pragma unroll
@@ -463,7 +469,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             for (int u = 0; u < NB; ++u) {
                 const int t = tile + u * step;
                 if (t >= tile_end) break;
-                if (oka[u] || okb[u]) process(fa[u], fb[u], oka[u], okb[u], t);
+                if (oka[u] > 0 || okb[u] > 0) process(fa[u], fb[u], oka[u], okb[u], t);
                 const int nt = t + NB * step;
                 oka[u] = load(nt, fa[u]);
                 okb[u] = load(nt + 1, fb[u]);
@@ -493,20 +499,26 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 #define VSPEC_I4_PAIRS_IN_FLIGHT 1
 #endif
 
-template <int D, int GW>
-void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
+template <int D, int GW, bool USED>
+void launch_used(const DecodeParams& p, dim3 grid, hipStream_t s) {
     constexpr int NB = VSPEC_I4_PAIRS_IN_FLIGHT;
     if (p.read_flags) {
         if (p.block_tokens == 16)
-            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB, true>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB, true, USED>), grid, dim3(256), 0, s, p);
         else
-            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, true>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, true, USED>), grid, dim3(256), 0, s, p);
     } else {
         if (p.block_tokens == 16)
-            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB, false>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB, false, USED>), grid, dim3(256), 0, s, p);
         else
-            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, false>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, false, USED>), grid, dim3(256), 0, s, p);
     }
+}
+
+template <int D, int GW>
+void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
+    if (p.block_used) launch_used<D, GW, true>(p, grid, s);
+    else launch_used<D, GW, false>(p, grid, s);
     // items split over several workgroups (same split: equal shares)
     const dim3 merge_grid(p.batch * p.hkv * p.gsplit);
     hipLaunchKernelGGL((decode_merge_split<D, GW, false>), merge_grid, dim3(kWaves * 64), 0, s, p);

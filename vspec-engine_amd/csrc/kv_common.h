@@ -187,6 +187,7 @@ struct DecodeParams {
     bool read_flags;     // the decode takes the flags instead of screening every tile
     const int32_t* block_tables;
     const int32_t* ctx_lens;
+    const int32_t* block_used;  // [B][max_blocks] tokens per table entry's block, or null (full)
     const float* q;
     float* out;
     float* part_ml;    // [B][Hq][max_parts][2] (max in log2 units, sum)
@@ -315,6 +316,10 @@ __device__ __forceinline__ int item_tiles(const DecodeParams& p, int b) {
     const int ctx = min(max(as_const(p.ctx_lens)[b], 0), (int)(p.max_blocks * p.block_tokens));
     return max(1, min((ctx + kTile - 1) / kTile, (int)p.max_tiles));
 }
+
+// Valid tokens of a 16-token tile whose block holds `used` tokens (slots 0 .. used-1) and
+// whose first slot in that block is slot0.
+__device__ __forceinline__ int used_cap(int used, int slot0) { return min(kTile, max(0, used - slot0)); }
 
 // First tile of workgroup g.  The balanced split gives workgroup g the tiles
 // [C(g) T / W, C(g+1) T / W) with C the cumulative share: equal shares, or, with a grid

@@ -196,6 +196,11 @@ __global__ __launch_bounds__(256, 2) void decode_partial(DecodeParams p) {
         const size_t row0 = ((size_t)phys * p.hkv + hk) * p.block_tokens +
                             (size_t)(tile % tiles_per_block) * kTile;
         const int tok0 = tile * kTile;
+        // valid slots of this tile: below the context and, with block_used, below its
+        // block's used count (a prefix of the block's slots)
+        const int lim = p.block_used ? min(ctx - tok0, used_cap(p.block_used[(size_t)b * p.max_blocks + lblock],
+                                                                (tile % tiles_per_block) * kTile))
+                                     : ctx - tok0;
 
         // ---- scores ----
         float s[KPASS][GW];
@@ -205,7 +210,7 @@ __global__ __launch_bounds__(256, 2) void decode_partial(DecodeParams p) {
             float x[16];
             load_k16<DT, D>(p, row0 + slot, sub, x);
             clamp_row<LPK, D>(x, p.alpha, p.input_clip);
-            const bool valid = tok0 + slot < ctx;
+            const bool valid = slot < lim;
 #pragma unroll
             for (int h = 0; h < GW; ++h) {
                 float d = 0.f;
@@ -253,13 +258,13 @@ __global__ __launch_bounds__(256, 2) void decode_partial(DecodeParams p) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
         // ---- P.V ----
-        const bool tail = tok0 + kTile > ctx;
+        const bool tail = lim < kTile;
 #pragma unroll
         for (int vp = 0; vp < VPASS; ++vp) {
             const int slot = vp * VTPP + vt;
             float x[8];
             load_v8<DT, D>(p, row0 + slot, vc, x);
-            if (tail && tok0 + slot >= ctx) {
+            if (tail && slot >= lim) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[e] = 0.f;
             }
@@ -1362,6 +1367,7 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.read_flags = p.kf && pl.split && pl.split_tiles >= (uint64_t)decode_flag_min_tiles() * pl.grid_x;
     p.block_tables = desc->block_tables;
     p.ctx_lens = desc->ctx_lens;
+    p.block_used = desc->block_used;
     p.q = desc->q;
     p.out = desc->out;
     p.part_ml = (float*)ws;

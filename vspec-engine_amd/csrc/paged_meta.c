@@ -210,8 +210,10 @@ int vspec_rocm_paged_reuse_prefix(VspecRocmPagedMeta* m, uint64_t target, uint64
     return 1;
 }
 
-int vspec_rocm_paged_reserve(VspecRocmPagedMeta* m, uint64_t id, uint32_t* page_out,
-                             uint32_t* slot_out) {
+/* The bookkeeping of one append; also reports the page's index in the session's list,
+ * which locates the token in table-slot space (index * page_tokens + slot). */
+static int reserve_token(VspecRocmPagedMeta* m, uint64_t id, uint32_t* page_out, uint32_t* slot_out,
+                         size_t* index_out) {
     if (!m) return 0;
     int slot = find_session(m, id);
     if (slot < 0) {
@@ -237,11 +239,16 @@ int vspec_rocm_paged_reserve(VspecRocmPagedMeta* m, uint64_t id, uint32_t* page_
     }
     if (page_out) *page_out = (uint32_t)p;
     if (slot_out) *slot_out = m->page[p].used_tokens;
+    if (index_out) *index_out = s->page_count - 1u;
     m->page[p].used_tokens += 1u;
     m->page[p].last_touch_step = m->clock_step;
     s->total_tokens += 1u;
     m->stats.append_token_count += 1u;
     return 1;
+}
+
+int vspec_rocm_paged_reserve(VspecRocmPagedMeta* m, uint64_t id, uint32_t* page_out, uint32_t* slot_out) {
+    return reserve_token(m, id, page_out, slot_out, NULL);
 }
 
 int vspec_rocm_paged_locate(const VspecRocmPagedMeta* m, uint64_t id, size_t token_idx,
@@ -306,6 +313,26 @@ int vspec_rocm_paged_page_info(const VspecRocmPagedMeta* m, size_t page, uint32_
     return 1;
 }
 
+int vspec_rocm_paged_block_layout(const VspecRocmPagedMeta* m, uint64_t id, int32_t* blocks, int32_t* used,
+                                  size_t cap, uint32_t* span, uint32_t* tokens) {
+    const int slot = find_session(m, id);
+    if (slot < 0 || !blocks || !used) return 0;
+    const Session* s = &m->session[slot];
+    if (s->page_count > cap) return 0;
+    if (s->page_count && s->page_count * m->page_tokens > (size_t)INT32_MAX) return 0;
+    uint32_t last_used = 0u;
+    for (size_t i = 0; i < s->page_count; ++i) {
+        const uint32_t p = s->pages[i];
+        if (p >= m->max_pages || p > (uint32_t)INT32_MAX) return 0;
+        blocks[i] = (int32_t)p;
+        used[i] = (int32_t)m->page[p].used_tokens;
+        last_used = m->page[p].used_tokens;
+    }
+    if (span) *span = s->page_count ? (uint32_t)((s->page_count - 1u) * m->page_tokens + last_used) : 0u;
+    if (tokens) *tokens = (uint32_t)s->total_tokens;
+    return 1;
+}
+
 int vspec_rocm_paged_block_table(const VspecRocmPagedMeta* m, uint64_t id, int32_t* out,
                                  size_t cap, uint32_t* ctx_len) {
     const int slot = find_session(m, id);
@@ -325,15 +352,19 @@ int vspec_rocm_paged_block_table(const VspecRocmPagedMeta* m, uint64_t id, int32
 /* One continuous-batching step (the items of vspec_continuous_batch_next_batch,
  * continuous_batch.c:155-270): reserve every item's token_quota new tokens, then emit
  * the kernels' inputs.  Items are processed in order; item i's new tokens are packed
- * at [sum of earlier quotas, + quota).  Fails when an item repeats a request, a
- * reservation fails, a later reservation evicted an earlier item's session, a session
- * cannot be expressed as a block table (a shared, partly filled page in the middle),
- * or an output is too small.  Reservations made before a failure stay made, as with a
- * sequence of reference appends that stops at its first failure. */
+ * at [sum of earlier quotas, + quota).  Positions are in table-slot space (page index in
+ * the session * page_tokens + slot), which equals the token index while every page but
+ * the last is full.  With block_used, every session is expressed (ctx_lens = span,
+ * block_used = per-entry used counts); without it, a session whose shared, partly filled
+ * page sits in the middle fails the step.  Also fails when an item repeats a request, a
+ * reservation fails, a later reservation evicted an earlier item's session, or an output
+ * is too small.  Reservations made before a failure stay made, as with a sequence of
+ * reference appends that stops at its first failure. */
 int vspec_rocm_paged_plan_step(VspecRocmPagedMeta* m, const VspecRocmStepItem* items,
-                               size_t n_items, int32_t* block_tables, size_t max_blocks,
-                               int32_t* ctx_lens, int32_t* start_pos, int32_t* token_item,
-                               int32_t* token_pos, size_t max_tokens, size_t* n_tokens) {
+                               size_t n_items, int32_t* block_tables, int32_t* block_used,
+                               size_t max_blocks, int32_t* ctx_lens, int32_t* start_pos,
+                               int32_t* token_item, int32_t* token_pos, size_t max_tokens,
+                               size_t* n_tokens) {
     if (!m || (n_items && (!items || !block_tables || !ctx_lens || !start_pos)) || max_blocks == 0) {
         return 0;
     }
@@ -346,30 +377,61 @@ int vspec_rocm_paged_plan_step(VspecRocmPagedMeta* m, const VspecRocmStepItem* i
         total += items[i].token_quota;
     }
     if (total && (!token_item || !token_pos)) return 0;
+    size_t* before = (size_t*)calloc(n_items ? n_items : 1u, sizeof(size_t));
+    if (!before) return 0;
+    int ok = 1;
     size_t off = 0;
-    for (size_t i = 0; i < n_items; ++i) {
+    for (size_t i = 0; ok && i < n_items; ++i) {
         const uint64_t id = items[i].request_id;
-        if (!vspec_rocm_paged_open_session(m, id)) return 0;
-        const size_t before = vspec_rocm_paged_session_tokens(m, id);
-        if (before + items[i].token_quota > (size_t)INT32_MAX) return 0;
-        start_pos[i] = (int32_t)before;
+        if (!vspec_rocm_paged_open_session(m, id)) {
+            ok = 0;
+            break;
+        }
+        before[i] = vspec_rocm_paged_session_tokens(m, id);
         for (size_t t = 0; t < items[i].token_quota; ++t) {
-            if (!vspec_rocm_paged_reserve(m, id, NULL, NULL)) return 0;
+            uint32_t slot = 0u;
+            size_t index = 0u;
+            if (!reserve_token(m, id, NULL, &slot, &index)) {
+                ok = 0;
+                break;
+            }
+            const size_t pos = index * m->page_tokens + slot;
+            if (pos > (size_t)INT32_MAX) {
+                ok = 0;
+                break;
+            }
+            if (t == 0) start_pos[i] = (int32_t)pos;
             token_item[off + t] = (int32_t)i;
-            token_pos[off + t] = (int32_t)(before + t);
+            token_pos[off + t] = (int32_t)pos;
+        }
+        if (ok && items[i].token_quota == 0u) {
+            /* no new token: the next free position in table-slot space */
+            const Session* s = &m->session[find_session(m, id)];
+            const size_t last = s->page_count ? m->page[s->pages[s->page_count - 1u]].used_tokens : 0u;
+            start_pos[i] = (int32_t)(s->page_count ? (s->page_count - 1u) * m->page_tokens + last : 0u);
         }
         off += items[i].token_quota;
     }
-    for (size_t i = 0; i < n_items; ++i) {
+    for (size_t i = 0; ok && i < n_items; ++i) {
         const uint64_t id = items[i].request_id;
         /* an eviction triggered by a later item restarts this session's count */
-        if (vspec_rocm_paged_session_tokens(m, id) != (size_t)start_pos[i] + items[i].token_quota) return 0;
+        if (vspec_rocm_paged_session_tokens(m, id) != before[i] + items[i].token_quota) {
+            ok = 0;
+            break;
+        }
         int32_t* row = block_tables + i * max_blocks;
         for (size_t k = 0; k < max_blocks; ++k) row[k] = -1;
         uint32_t ctx = 0;
-        if (!vspec_rocm_paged_block_table(m, id, row, max_blocks, &ctx)) return 0;
+        if (block_used) {
+            int32_t* urow = block_used + i * max_blocks;
+            for (size_t k = 0; k < max_blocks; ++k) urow[k] = 0;
+            ok = vspec_rocm_paged_block_layout(m, id, row, urow, max_blocks, &ctx, NULL);
+        } else {
+            ok = vspec_rocm_paged_block_table(m, id, row, max_blocks, &ctx);
+        }
         ctx_lens[i] = (int32_t)ctx;
     }
-    if (n_tokens) *n_tokens = total;
-    return 1;
+    free(before);
+    if (ok && n_tokens) *n_tokens = total;
+    return ok;
 }

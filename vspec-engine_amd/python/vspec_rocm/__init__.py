@@ -57,6 +57,7 @@ class VspecPagedAttnDesc(C.Structure):
         ("workspace", _vp),
         ("workspace_bytes", C.c_size_t),
         ("stream", _vp),
+        ("block_used", _vp),
     ]
 
 
@@ -176,6 +177,7 @@ SIGNATURES = {
     "vspec_rocm_paged_session_pages": (C.c_size_t, [_vp, C.c_uint64, _u32p, C.c_size_t]),
     "vspec_rocm_paged_page_info": (C.c_int, [_vp, C.c_size_t, _u32p, _u32p, _u32p]),
     "vspec_rocm_paged_block_table": (C.c_int, [_vp, C.c_uint64, _i32p_, C.c_size_t, _u32p]),
+    "vspec_rocm_paged_block_layout": (C.c_int, [_vp, C.c_uint64, _i32p_, _i32p_, C.c_size_t, _u32p, _u32p]),
     "vspec_py_kv_cache_create": (C.c_int, [C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t]),
     "vspec_py_kv_cache_destroy": (None, [C.c_int]),
     "vspec_py_kv_cache_reset": (C.c_int, [C.c_int]),
@@ -185,8 +187,8 @@ SIGNATURES = {
     "vspec_py_kv_cache_meta": (_vp, [C.c_int]),
     "vspec_py_kv_cache_pool": (C.POINTER(VspecPagedKV), [C.c_int]),
     "vspec_rocm_kv_gather_rows": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, _vp, _vp]),
-    "vspec_rocm_paged_plan_step": (C.c_int, [_vp, C.POINTER(VspecRocmStepItem), C.c_size_t, _i32p_, C.c_size_t, _i32p_,
-                                             _i32p_, _i32p_, _i32p_, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "vspec_rocm_paged_plan_step": (C.c_int, [_vp, C.POINTER(VspecRocmStepItem), C.c_size_t, _i32p_, _i32p_, C.c_size_t,
+                                             _i32p_, _i32p_, _i32p_, _i32p_, C.c_size_t, C.POINTER(C.c_size_t)]),
     "vspec_rocm_kv_append_tokens": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, C.c_uint32,
                                               C.c_uint32, _vp, _vp, C.c_int32, _vp]),
     "vspec_rocm_release_retired_workspaces": (C.c_int, []),
@@ -433,7 +435,8 @@ def kv_compact(pool: PagedPool, src_blocks, dst_blocks, stream=None):
 
 
 def make_decode_desc(pool: PagedPool, block_tables, ctx_lens, q, out, max_ctx_len, numerics=NUMERICS_PLAIN,
-                     scale=0.0, partition_tokens=0, workspace=None, stream=None) -> VspecPagedAttnDesc:
+                     scale=0.0, partition_tokens=0, workspace=None, stream=None,
+                     block_used=None) -> VspecPagedAttnDesc:
     B, Hq, D = q.shape
     d = VspecPagedAttnDesc()
     d.kv = pool.desc()
@@ -446,6 +449,7 @@ def make_decode_desc(pool: PagedPool, block_tables, ctx_lens, q, out, max_ctx_le
     if workspace is not None:
         d.workspace, d.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     d.stream = _stream(stream)
+    d.block_used = _ptr(block_used)
     return d
 
 
@@ -454,26 +458,29 @@ def decode_workspace_bytes(desc: VspecPagedAttnDesc) -> int:
 
 
 def paged_decode(pool: PagedPool, block_tables, ctx_lens, q, max_ctx_len=None, numerics=NUMERICS_PLAIN,
-                 scale=0.0, partition_tokens=0, out=None, workspace=None, stream=None):
-    """vspec_rocm_paged_decode_attention: q [B][Hq][D] float32 (device) -> out."""
+                 scale=0.0, partition_tokens=0, out=None, workspace=None, stream=None, block_used=None):
+    """vspec_rocm_paged_decode_attention: q [B][Hq][D] float32 (device) -> out.  With
+    block_used ([B][max_blocks], tokens per table entry) ctx_lens holds the spans."""
     import torch
 
     assert q.dtype == torch.float32 and q.is_contiguous()
     bt = _i32(block_tables, pool.device)
     cl = _i32(ctx_lens, pool.device)
+    bu = None if block_used is None else _i32(block_used, pool.device)
+    assert bu is None or bu.shape == bt.shape
     if max_ctx_len is None:
         max_ctx_len = int(cl.max().item()) if cl.numel() else 0
     if out is None:
         out = torch.empty_like(q)
-    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream)
+    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream, bu)
     _check(lib().vspec_rocm_paged_decode_attention(C.byref(d)), "paged_decode_attention")
-    _hold(stream, bt, cl, out)
+    _hold(stream, bt, cl, bu, out)
     return out
 
 
 def paged_decode_step(pool: PagedPool, block_tables, ctx_lens, q, k_new, v_new, max_ctx_len=None,
                       numerics=NUMERICS_PLAIN, scale=0.0, partition_tokens=0, out=None, workspace=None,
-                      stream=None):
+                      stream=None, block_used=None):
     """vspec_rocm_paged_decode_step: append k_new / v_new [B][Hkv][D] (float32 or float16,
     device) at position ctx_lens[b] - 1, then decode q [B][Hq][D] float32 -> out."""
     import torch
@@ -484,14 +491,16 @@ def paged_decode_step(pool: PagedPool, block_tables, ctx_lens, q, k_new, v_new, 
     src = KV_F32 if k_new.dtype == torch.float32 else KV_F16
     bt = _i32(block_tables, pool.device)
     cl = _i32(ctx_lens, pool.device)
+    bu = None if block_used is None else _i32(block_used, pool.device)
+    assert bu is None or bu.shape == bt.shape
     if max_ctx_len is None:
         max_ctx_len = int(cl.max().item()) if cl.numel() else 0
     if out is None:
         out = torch.empty_like(q)
-    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream)
+    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream, bu)
     _check(lib().vspec_rocm_paged_decode_step(C.byref(d), k_new.data_ptr(), v_new.data_ptr(), src),
            "paged_decode_step")
-    _hold(stream, bt, cl, out)
+    _hold(stream, bt, cl, bu, out)
     return out
 
 

@@ -122,6 +122,20 @@ class CorePagedKVCache:
                                                 C.byref(ctx))
         return (tab, int(ctx.value)) if ok else None
 
+    def block_layout(self, session_id: int, max_blocks: int):
+        """Any session as (int32 table [max_blocks] padded with -1, int32 used counts
+        [max_blocks], span, tokens): the decode inputs with block_used, which also cover
+        shared, partly filled pages in the middle of a session."""
+        tab = np.full(max_blocks, -1, np.int32)
+        used = np.zeros(max_blocks, np.int32)
+        span, tokens = C.c_uint32(), C.c_uint32()
+        p32 = lambda a: a.ctypes.data_as(C.POINTER(C.c_int32))
+        ok = lib().vspec_rocm_paged_block_layout(self._meta(), int(session_id), p32(tab), p32(used), max_blocks,
+                                                 C.byref(span), C.byref(tokens))
+        if not ok:
+            raise VspecRocmError(f"block_layout: unknown session {session_id} or more than {max_blocks} pages")
+        return tab, used, int(span.value), int(tokens.value)
+
     def device_pool(self) -> HandlePool:
         p = lib().vspec_py_kv_cache_pool(self.handle)
         if not p:
@@ -140,13 +154,14 @@ class CorePagedKVCache:
             pass
 
 
-def plan_step(meta, items, max_blocks: int, max_tokens: int | None = None):
+def plan_step(meta, items, max_blocks: int, max_tokens: int | None = None, with_used: bool = False):
     """vspec_rocm_paged_plan_step over a VspecRocmPagedMeta* (e.g. CorePagedKVCache._meta()).
 
     items: sequence of (request_id, phase, token_quota, prompt_cursor) or VspecRocmStepItem.
     Returns dict(block_tables [n][max_blocks], ctx_lens [n], start_pos [n], token_item [t],
-    token_pos [t]) as int32 numpy arrays; raises VspecRocmError when the step cannot be
-    planned."""
+    token_pos [t]) as int32 numpy arrays, positions in table-slot space; with_used adds
+    block_used [n][max_blocks] (ctx_lens then hold spans) and accepts sessions with partly
+    filled middle pages.  Raises VspecRocmError when the step cannot be planned."""
     n = len(items)
     arr = (VspecRocmStepItem * max(n, 1))()
     for i, it in enumerate(items):
@@ -161,13 +176,17 @@ def plan_step(meta, items, max_blocks: int, max_tokens: int | None = None):
     start = np.zeros(max(n, 1), np.int32)
     titem = np.zeros(max(cap, 1), np.int32)
     tpos = np.zeros(max(cap, 1), np.int32)
+    used = np.zeros((max(n, 1), max_blocks), np.int32) if with_used else None
     got = C.c_size_t()
-    p32 = lambda a: a.ctypes.data_as(C.POINTER(C.c_int32))
-    ok = lib().vspec_rocm_paged_plan_step(meta, arr, n, p32(tables), max_blocks, p32(ctx), p32(start), p32(titem),
-                                          p32(tpos), cap, C.byref(got))
+    p32 = lambda a: None if a is None else a.ctypes.data_as(C.POINTER(C.c_int32))
+    ok = lib().vspec_rocm_paged_plan_step(meta, arr, n, p32(tables), p32(used), max_blocks, p32(ctx), p32(start),
+                                          p32(titem), p32(tpos), cap, C.byref(got))
     if not ok:
         raise VspecRocmError("plan_step failed (pool exhausted, eviction of a batch member, repeated request, "
                              "shared partly filled page, or outputs too small)")
     t = int(got.value)
-    return dict(block_tables=tables[:n], ctx_lens=ctx[:n], start_pos=start[:n], token_item=titem[:t],
-                token_pos=tpos[:t])
+    out = dict(block_tables=tables[:n], ctx_lens=ctx[:n], start_pos=start[:n], token_item=titem[:t],
+               token_pos=tpos[:t])
+    if with_used:
+        out["block_used"] = used[:n]
+    return out
