@@ -376,6 +376,58 @@ def run_c5(args, wl, kv_dtype, mode):
     }
 
 
+def run_legacy(args):
+    """The legacy registry path: launch_attention with a host VspecKVCache (fp32 [T][H][D]
+    rows, the reference context convention of cpu_backend.c:40-51) in a decode loop that
+    appends one token per call, as vspec_attention_forward drives it.  Times the calls with
+    the persistent device mirror (only the new rows uploaded) and with the mirror released
+    before every call (the whole cache uploaded, as a per-call copy does)."""
+    import ctypes as C
+
+    import numpy as np
+
+    import vspec_rocm as vr
+
+    T, H, D = args.legacy_tokens, 8, 128
+    steps = max(args.steps, 10)
+    rng = np.random.default_rng(args.seed)
+    cap = T + steps + args.warmup + max(5, steps // 10) + 2
+    kb = rng.standard_normal((cap, H, D)).astype(np.float32)
+    vb = rng.standard_normal((cap, H, D)).astype(np.float32)
+    q = rng.standard_normal((H, D)).astype(np.float32)
+    out = np.zeros((H, D), np.float32)
+    cache = vr.VspecKVCache()
+    cache.key, cache.value = kb.ctypes.data, vb.ctypes.data
+    cache.max_tokens, cache.num_heads, cache.head_dim, cache.current_tokens = cap, H, D, T
+    ctx = vr.VspecKernelContext()
+    ctx.input, ctx.weight, ctx.output = q.ctypes.data, C.cast(C.pointer(cache), C.c_void_p), out.ctypes.data
+    be = vr.backend()
+    L = vr.lib()
+    cptr = C.cast(C.pointer(cache), C.c_void_p)
+
+    def loop(n, release):
+        t0 = time.perf_counter()
+        for _ in range(n):
+            cache.current_tokens += 1
+            if release:
+                L.vspec_rocm_release_cache_mirror(cptr)
+            out[:] = 7.0
+            be.launch_attention(C.byref(ctx))
+            if out[0, 0] == 7.0:
+                raise vr.VspecRocmError(vr.last_error())
+        return (time.perf_counter() - t0) / n
+
+    loop(args.warmup, False)
+    mirror = loop(steps, False)
+    full = loop(max(5, steps // 10), True)
+    L.vspec_rocm_release_cache_mirror(cptr)
+    return {"metric": "legacy launch_attention latency (host VspecKVCache, one appended token per call)",
+            "value": mirror * 1e6, "unit": "us/call", "higher_is_better": False, "n_gpus": 1,
+            "config": {"workload": f"legacy-ctx{T}", "tokens": T, "heads": H, "head_dim": D, "kv": "f32 host rows"},
+            "mirror_us_per_call": mirror * 1e6, "full_upload_us_per_call": full * 1e6,
+            "note": "mirror: only the appended rows are uploaded; full: the mirror is released before each call"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -393,6 +445,9 @@ def main():
                     help="print the HBM bandwidth probes (copy, random/sequential tile reads) and exit")
     ap.add_argument("--no-probe", action="store_true",
                     help="skip the probe ceilings in the bench line")
+    ap.add_argument("--legacy", action="store_true",
+                    help="time the legacy registry path (launch_attention over a host VspecKVCache) and exit")
+    ap.add_argument("--legacy-tokens", type=int, default=4096)
     ap.add_argument("--separate-append", action="store_true",
                     help="append with its own launch before the decode launch (timed: the decode)")
     ap.add_argument("--batch", type=int, default=0,
@@ -417,6 +472,9 @@ def main():
 
     vr.lib()
     dev = torch.device("cuda:0")
+    if args.legacy:
+        print(json.dumps(run_legacy(args)), flush=True)
+        return
     if args.probe:
         print(json.dumps({"metric": "HBM bandwidth probes", "unit": "GB/s", "peak": PEAK_GBS,
                           **probe_ceilings(dev), **{"host": host_cpu()}}), flush=True)

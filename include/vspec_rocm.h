@@ -180,6 +180,14 @@ int vspec_rocm_sync(void* stream);
 const char* vspec_rocm_last_error(void);
 int vspec_rocm_device_count(void);
 
+/* The legacy contiguous-cache path (launch_attention with a host VspecKVCache*) keeps a
+ * device mirror per cache so that each call uploads only the rows appended since the
+ * previous one (kv_cache.c:160-226 appends only).  Call this when a cache is destroyed,
+ * or when its rows are rewritten in place rather than appended (a shrunk current_tokens
+ * or changed first/last synced rows are detected; other in-place edits are not), to free
+ * the mirror's device memory; NULL releases every mirror.  Returns 1. */
+int vspec_rocm_release_cache_mirror(const VspecKVCache* cache);
+
 /* ---- backend registry entry: replaces rocm_backend_stub.c:3-21 ----
  * launch_attention accepts either the reference context (ctx->input host q [H][D],
  * ctx->weight const VspecKVCache*, ctx->output host out [H][D]; cpu_backend.c:40-51)

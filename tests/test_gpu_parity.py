@@ -1334,6 +1334,50 @@ def test_backend_int3_cache_without_mirror(oracle, gpu, D, block_size, mode):
             assert np.array_equal(out.view(np.uint32), ref_out.view(np.uint32)), mirror
 
 
+@pytest.mark.parametrize("D", [128, 20])
+def test_backend_decode_loop_appends_only(oracle, gpu, D):
+    """A 64-step decode loop through the registry entry, as vspec_attention_forward
+    (runtime.c:641-647) drives it: each step appends one token to the host VspecKVCache
+    (kv_cache.c:160-226) and calls launch_attention.  The device mirror uploads only the
+    appended rows; every step matches the oracle's attention_ref over all rows so far.
+    Then the cache is rewound (current_tokens shrinks) and refilled with other rows at the
+    same addresses: the mirror resyncs and the results follow the new rows."""
+    import ctypes as C
+    import vspec_rocm as vr
+
+    H, T0, steps = 8, 700, 64
+    cap = T0 + steps
+    k = np.ascontiguousarray(oracle.normal(600 + D, cap * H * D).reshape(cap, H, D))
+    v = np.ascontiguousarray(oracle.normal(601 + D, cap * H * D).reshape(cap, H, D))
+    q_all = oracle.normal(602 + D, steps * H * D).reshape(steps, H, D)
+    kb, vb = np.zeros_like(k), np.zeros_like(v)  # the cache's host buffers
+    kb[:T0], vb[:T0] = k[:T0], v[:T0]
+    cache = vr.VspecKVCache()
+    cache.key, cache.value = kb.ctypes.data, vb.ctypes.data
+    cache.max_tokens, cache.num_heads, cache.head_dim, cache.current_tokens = cap, H, D, T0
+    try:
+        worst = 0.0
+        for i in range(steps):
+            t = T0 + i
+            kb[t], vb[t] = k[t], v[t]
+            cache.current_tokens = t + 1
+            mode = i % 2
+            out, err = _launch_cache(q_all[i], cache, mode)
+            want = oracle.attention_ref(mode, q_all[i], kb[: t + 1], vb[: t + 1])
+            worst = max(worst, float(np.abs(out - want).max()))
+            assert np.abs(out - want).max() <= 2e-5, (i, np.abs(out - want).max(), err)
+        say(f"[legacy loop] D={D} steps={steps} max-abs {worst:.2e}")
+        # rewind and refill the same buffers with other rows
+        kb[:] = -k[::-1]
+        vb[:] = v[::-1]
+        cache.current_tokens = 300
+        out, err = _launch_cache(q_all[0], cache, 1)
+        want = oracle.attention_ref(1, q_all[0], kb[:300], vb[:300])
+        assert np.abs(out - want).max() <= 2e-5, (np.abs(out - want).max(), err)
+    finally:
+        assert vr.lib().vspec_rocm_release_cache_mirror(C.cast(C.pointer(cache), C.c_void_p)) == 1
+
+
 def test_backend_int3_cache_rejects_bad_geometry(oracle, gpu):
     """A codec-only cache whose block_size is 0 or whose code rows are too short for
     head_dim is refused with an error; the output is left as it was."""

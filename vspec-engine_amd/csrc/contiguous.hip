@@ -4,17 +4,19 @@
 // A VspecKVCache holds [T][H][D] keys and values in host memory: fp32 rows (also the fp32
 // mirror when the reference's int3 codec is on, kv_cache.c:198-215), or, for a cache whose
 // codec runs without a mirror, 3-bit codes with per-block fp32 scales that the reference's
-// accessors decode on every read (kv_cache.c:296-362).  Rows are uploaded as they are;
-// codes and scales are uploaded and decoded to fp32 on the device, bit for bit as the
-// reference decodes them.  For head_dim 64 / 128 the rows then go through the append
-// kernel into a temporary f32 paged pool with an identity block table and the decode
-// kernel runs with Hq == Hkv (MHA); other head sizes run a generic
-// one-workgroup-per-head kernel over the rows.
+// accessors decode on every read (kv_cache.c:296-362).  Each cache gets a persistent device
+// mirror (below): a call uploads only the rows appended since the previous call (codes and
+// scales are decoded to fp32 on the device, bit for bit as the reference decodes them).
+// For head_dim 64 / 128 the mirror is an f32 paged pool with an identity block table that
+// the decode kernels read with Hq == Hkv (MHA); other head sizes run a generic
+// one-workgroup-per-head kernel over device rows.
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+
+#include <mutex>
 
 #include "vspec_rocm.h"
 
@@ -142,87 +144,6 @@ __global__ __launch_bounds__(kThreads) void int3_rows_to_f32(Int3Rows p) {
     }
 }
 
-// Attention over [T][H][D] fp32 rows already in device memory, q and out in host memory.
-// head_dim 64 / 128: the rows go through the append kernel into a temporary f32 paged
-// pool (identity block table) and the decode kernel runs with Hq == Hkv; other head sizes
-// take the generic kernel above.
-int attention_rows(const float* q, const float* d_k, const float* d_v, size_t tokens, size_t heads,
-                   size_t head_dim, int32_t numerics, float* out) {
-    const size_t q_bytes = heads * head_dim * sizeof(float);
-    if (head_dim != 64 && head_dim != 128) {
-        void *d_q = nullptr, *d_o = nullptr, *d_s = nullptr;
-        int ok = hipMalloc(&d_q, q_bytes) == hipSuccess && hipMalloc(&d_o, q_bytes) == hipSuccess &&
-                 hipMalloc(&d_s, tokens * heads * sizeof(float)) == hipSuccess &&
-                 hipMemcpy(d_q, q, q_bytes, hipMemcpyHostToDevice) == hipSuccess;
-        if (!ok) vspec_rocm_set_error_("attention: device allocation or upload failed");
-        if (ok) {
-            const bool three = numerics == VSPEC_NUMERICS_3BIT;
-            float scale = 1.0f / sqrtf((float)head_dim);
-            if (three) scale = fminf(fmaxf(scale, 1e-4f), 32.0f);
-            ContigParams p = {(const float*)d_q, d_k, d_v, (float*)d_o, (float*)d_s,
-                              (uint32_t)tokens, (uint32_t)heads, (uint32_t)head_dim, scale * kLog2e, 4.5f,
-                              three ? 24.0f * kLog2e : INFINITY, three ? 16.0f : INFINITY};
-            const size_t smem = (kThreads + head_dim) * sizeof(float);
-            hipLaunchKernelGGL(attention_contig, dim3((unsigned)heads), dim3(kThreads), smem, nullptr, p);
-            ok = hipGetLastError() == hipSuccess &&
-                 hipMemcpy(out, d_o, q_bytes, hipMemcpyDeviceToHost) == hipSuccess;
-            if (!ok) vspec_rocm_set_error_("attention: launch or download failed");
-        }
-        (void)hipFree(d_q);
-        (void)hipFree(d_o);
-        (void)hipFree(d_s);
-        return ok;
-    }
-    const uint32_t P = 16;
-    const uint32_t nblk = (uint32_t)((tokens + P - 1) / P);
-    VspecPagedKV kv;
-    if (!vspec_rocm_kv_pool_create(&kv, VSPEC_KV_F32, nblk, P, (uint32_t)heads, (uint32_t)head_dim)) {
-        return 0;
-    }
-    int32_t* h_tab = (int32_t*)malloc(nblk * sizeof(int32_t));
-    void *d_q = nullptr, *d_o = nullptr, *d_tab = nullptr, *d_misc = nullptr;
-    int ok = h_tab != nullptr;
-    if (ok) {
-        for (uint32_t i = 0; i < nblk; ++i) h_tab[i] = (int32_t)i;
-    }
-    ok = ok && hipMalloc(&d_q, q_bytes) == hipSuccess && hipMalloc(&d_o, q_bytes) == hipSuccess &&
-         hipMalloc(&d_tab, nblk * sizeof(int32_t)) == hipSuccess &&
-         hipMalloc(&d_misc, 2 * sizeof(int32_t)) == hipSuccess;
-    int32_t misc[2] = {0, (int32_t)tokens};  // start_pos, ctx_len
-    ok = ok && hipMemcpy(d_q, q, q_bytes, hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(d_tab, h_tab, nblk * sizeof(int32_t), hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(d_misc, misc, sizeof(misc), hipMemcpyHostToDevice) == hipSuccess;
-    if (!ok) vspec_rocm_set_error_("attention: device allocation or upload failed");
-    ok = ok && vspec_rocm_kv_append(&kv, 1, (const int32_t*)d_tab, nblk, (const int32_t*)d_misc,
-                                    (uint32_t)tokens, d_k, d_v, VSPEC_KV_F32, nullptr);
-    if (ok) {
-        VspecPagedAttnDesc d;
-        memset(&d, 0, sizeof(d));
-        d.kv = kv;
-        d.batch = 1;
-        d.num_q_heads = (uint32_t)heads;
-        d.block_tables = (const int32_t*)d_tab;
-        d.max_blocks_per_seq = nblk;
-        d.ctx_lens = (const int32_t*)d_misc + 1;
-        d.max_ctx_len = (uint32_t)tokens;
-        d.q = (const float*)d_q;
-        d.out = (float*)d_o;
-        d.numerics = numerics;
-        ok = vspec_rocm_paged_decode_attention(&d);
-    }
-    if (ok && hipMemcpy(out, d_o, q_bytes, hipMemcpyDeviceToHost) != hipSuccess) {
-        vspec_rocm_set_error_("attention: download failed");
-        ok = 0;
-    }
-    (void)hipFree(d_q);
-    (void)hipFree(d_o);
-    (void)hipFree(d_tab);
-    (void)hipFree(d_misc);
-    free(h_tab);
-    vspec_rocm_kv_pool_destroy(&kv);
-    return ok;
-}
-
 // Where the reference's accessors read one side (key or value) of a cache from
 // (kv_cache.c:296-362): the fp32 rows whenever they exist (the plain cache, or the int3
 // codec's fp32 mirror), otherwise the int3 codes and scales when the codec is on.
@@ -241,39 +162,178 @@ CacheSide cache_side(const VspecKVCache* c, bool value) {
     return s;
 }
 
-// One side of the cache as device fp32 rows: an upload of the rows, or an upload of the
-// codes and scales followed by the decode kernel.
-int side_to_device(const VspecKVCache* c, const CacheSide& s, float* d_rows) {
-    const size_t tokens = c->current_tokens, rows = tokens * c->num_heads;
-    if (s.rows) {
-        if (hipMemcpy(d_rows, s.rows, rows * c->head_dim * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
-            vspec_rocm_set_error_("attention: upload of the cache rows failed");
-            return 0;
+// ---------------------------------------------------------------------------
+// Persistent device mirror of a host VspecKVCache.
+//
+// The reference's caches grow append-only between attention calls (kv_cache.c:160-226:
+// rows go to current_tokens and the count increments), so a mirror keyed by the cache
+// keeps the rows already uploaded and each call uploads only the rows appended since the
+// last one.  head_dim 64 / 128: the rows are appended into a persistent f32 paged pool
+// (identity block table, capacity max_tokens) and decoded by the paged kernels (Hq == Hkv);
+// other head sizes keep device [max_tokens][H][D] rows for the generic kernel.  Per call:
+// one upload of (q, the new rows or their int3 codes and scales) through pinned staging,
+// the int3 decode when needed, the append, the attention launches and one download of the
+// output; after a mirror's first call no device memory is allocated or freed unless the
+// new rows outgrow the staging buffers.
+//
+// A mirror is reused when the cache pointer, its buffer pointers and geometry are the
+// same, current_tokens did not shrink, and fingerprints of the first token's rows and of
+// the last synced token's rows still match; anything else resyncs from token 0.  A caller
+// that rewrites rows in place keeps the contract by calling
+// vspec_rocm_release_cache_mirror (also to free the device memory with the cache).
+// ---------------------------------------------------------------------------
+struct Mirror {
+    const VspecKVCache* cache = nullptr;
+    VspecKVCache shape;  // the cache fields at the last sync (pointers and geometry)
+    size_t synced = 0;   // tokens on the device
+    uint64_t fp_first = 0, fp_last = 0;
+    uint64_t last_use = 0;
+    bool paged = false;
+    VspecPagedKV kv;       // paged: persistent f32 pool
+    int32_t* d_tab = nullptr;
+    float* d_k = nullptr;  // generic: device rows [max_tokens][H][D]
+    float* d_v = nullptr;
+    float* d_scores = nullptr;
+    uint8_t* d_stage = nullptr;  // q, ctx/start, new rows (or codes + scales), decoded rows
+    size_t stage_bytes = 0;
+    uint8_t* h_stage = nullptr;  // pinned
+    size_t h_stage_bytes = 0;
+    float* d_out = nullptr;
+};
+
+constexpr int kMirrors = 16;
+Mirror g_mirror[kMirrors];
+uint64_t g_mirror_clock = 0;
+std::mutex g_mirror_mu;
+
+void mirror_free(Mirror& m) {
+    if (m.paged) vspec_rocm_kv_pool_destroy(&m.kv);
+    (void)hipFree(m.d_tab);
+    (void)hipFree(m.d_k);
+    (void)hipFree(m.d_v);
+    (void)hipFree(m.d_scores);
+    (void)hipFree(m.d_stage);
+    (void)hipFree(m.d_out);
+    if (m.h_stage) (void)hipHostFree(m.h_stage);
+    m = Mirror();
+}
+
+uint64_t fnv(uint64_t h, const void* p, size_t n) {
+    const uint8_t* b = (const uint8_t*)p;
+    for (size_t i = 0; i < n; ++i) h = (h ^ b[i]) * 1099511628211ull;
+    return h;
+}
+
+// fingerprint of token t's rows (both sides, every head; fp32 rows, or codes + scales)
+uint64_t token_fingerprint(const VspecKVCache* c, const CacheSide& ks, const CacheSide& vs, size_t t) {
+    uint64_t h = 1469598103934665603ull;
+    const size_t H = c->num_heads, D = c->head_dim;
+    for (const CacheSide* s : {&ks, &vs}) {
+        if (s->rows) {
+            h = fnv(h, s->rows + t * H * D, H * D * sizeof(float));
+        } else {
+            h = fnv(h, s->codes + t * H * c->packed_head_bytes, H * c->packed_head_bytes);
+            h = fnv(h, s->scales + t * H * c->blocks_per_head, H * c->blocks_per_head * sizeof(float));
         }
-        return 1;
     }
-    const size_t code_bytes = rows * c->packed_head_bytes;
-    const size_t scale_bytes = rows * c->blocks_per_head * sizeof(float);
-    void *d_codes = nullptr, *d_scales = nullptr;
-    int ok = hipMalloc(&d_codes, code_bytes) == hipSuccess && hipMalloc(&d_scales, scale_bytes) == hipSuccess &&
-             hipMemcpy(d_codes, s.codes, code_bytes, hipMemcpyHostToDevice) == hipSuccess &&
-             hipMemcpy(d_scales, s.scales, scale_bytes, hipMemcpyHostToDevice) == hipSuccess;
-    if (!ok) vspec_rocm_set_error_("attention: upload of the int3 codes failed");
-    if (ok) {
-        Int3Rows p = {(const uint8_t*)d_codes, (const float*)d_scales, d_rows, rows, c->packed_head_bytes,
-                      c->blocks_per_head, (uint32_t)c->head_dim, (uint32_t)c->block_size};
-        const size_t n = rows * c->head_dim;
-        const unsigned grid = (unsigned)((n + kThreads - 1) / kThreads < 8192 ? (n + kThreads - 1) / kThreads : 8192);
-        hipLaunchKernelGGL(int3_rows_to_f32, dim3(grid), dim3(kThreads), 0, nullptr, p);
-        ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(nullptr) == hipSuccess;
-        if (!ok) vspec_rocm_set_error_("attention: int3 decode failed");
+    return h;
+}
+
+bool same_shape(const VspecKVCache& a, const VspecKVCache& b) {
+    return a.key == b.key && a.value == b.value && a.max_tokens == b.max_tokens && a.num_heads == b.num_heads &&
+           a.head_dim == b.head_dim && a.int3_compressed == b.int3_compressed && a.key_int3 == b.key_int3 &&
+           a.value_int3 == b.value_int3 && a.key_scales == b.key_scales && a.value_scales == b.value_scales &&
+           a.block_size == b.block_size && a.blocks_per_head == b.blocks_per_head &&
+           a.packed_head_bytes == b.packed_head_bytes;
+}
+
+// device allocations that depend only on the cache's geometry (made once per mirror)
+int mirror_setup(Mirror& m, const VspecKVCache* c) {
+    const size_t T = c->max_tokens, H = c->num_heads, D = c->head_dim;
+    m.paged = D == 64 || D == 128;
+    const size_t qb = H * D * sizeof(float);
+    if (hipMalloc((void**)&m.d_out, qb) != hipSuccess) return 0;
+    if (m.paged) {
+        const uint32_t P = 16, nblk = (uint32_t)((T + P - 1) / P);
+        if (!vspec_rocm_kv_pool_create(&m.kv, VSPEC_KV_F32, nblk, P, (uint32_t)H, (uint32_t)D)) return 0;
+        int32_t* h_tab = (int32_t*)malloc(nblk * sizeof(int32_t));
+        if (!h_tab) return 0;
+        for (uint32_t i = 0; i < nblk; ++i) h_tab[i] = (int32_t)i;
+        const int ok = hipMalloc((void**)&m.d_tab, nblk * sizeof(int32_t)) == hipSuccess &&
+                       hipMemcpy(m.d_tab, h_tab, nblk * sizeof(int32_t), hipMemcpyHostToDevice) == hipSuccess;
+        free(h_tab);
+        return ok;
     }
-    (void)hipFree(d_codes);
-    (void)hipFree(d_scales);
-    return ok;
+    const size_t kvb = T * H * D * sizeof(float);
+    return hipMalloc((void**)&m.d_k, kvb) == hipSuccess && hipMalloc((void**)&m.d_v, kvb) == hipSuccess &&
+           hipMalloc((void**)&m.d_scores, T * H * sizeof(float)) == hipSuccess;
+}
+
+int grow(uint8_t** d, size_t* have, size_t need, bool pinned) {
+    if (*have >= need) return 1;
+    const size_t n = need + need / 4;
+    if (pinned) {
+        if (*d) (void)hipHostFree(*d);
+        *d = nullptr;
+        *have = 0;
+        if (hipHostMalloc((void**)d, n, hipHostMallocDefault) != hipSuccess) return 0;
+    } else {
+        if (*d) (void)hipFree(*d);
+        *d = nullptr;
+        *have = 0;
+        if (hipMalloc((void**)d, n) != hipSuccess) return 0;
+    }
+    *have = n;
+    return 1;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+Mirror* mirror_for(const VspecKVCache* c) {
+    Mirror* slot = nullptr;
+    for (Mirror& m : g_mirror) {
+        if (m.cache == c) {
+            slot = &m;
+            break;
+        }
+    }
+    if (slot && !same_shape(slot->shape, *c)) {
+        mirror_free(*slot);  // another cache (or other buffers) at this address
+        slot = nullptr;
+    }
+    if (!slot) {
+        for (Mirror& m : g_mirror) {
+            if (!m.cache && !slot) slot = &m;
+        }
+        if (!slot) {  // evict the least recently used
+            slot = &g_mirror[0];
+            for (Mirror& m : g_mirror) {
+                if (m.last_use < slot->last_use) slot = &m;
+            }
+            mirror_free(*slot);
+        }
+        if (!mirror_setup(*slot, c)) {
+            mirror_free(*slot);
+            vspec_rocm_set_error_("attention: device allocation for the cache mirror failed");
+            return nullptr;
+        }
+        slot->cache = c;
+        slot->shape = *c;
+        slot->synced = 0;
+    }
+    slot->last_use = ++g_mirror_clock;
+    return slot;
 }
 
 }  // namespace
+
+extern "C" int vspec_rocm_release_cache_mirror(const VspecKVCache* cache) {
+    std::lock_guard<std::mutex> lock(g_mirror_mu);
+    for (Mirror& m : g_mirror) {
+        if (m.cache && (cache == nullptr || m.cache == cache)) mirror_free(m);
+    }
+    return 1;
+}
 
 extern "C" int vspec_rocm_attention_cache_host(const float* q, const VspecKVCache* cache,
                                                int32_t numerics, float* out) {
@@ -282,6 +342,10 @@ extern "C" int vspec_rocm_attention_cache_host(const float* q, const VspecKVCach
         return 0;
     }
     const size_t tokens = cache->current_tokens, heads = cache->num_heads, head_dim = cache->head_dim;
+    if (tokens > cache->max_tokens) {
+        vspec_rocm_set_error_("attention: current_tokens exceeds max_tokens");
+        return 0;
+    }
     const CacheSide ks = cache_side(cache, false), vs = cache_side(cache, true);
     if ((!ks.rows && (!ks.codes || !ks.scales)) || (!vs.rows && (!vs.codes || !vs.scales))) {
         vspec_rocm_set_error_("attention: cache has neither fp32 rows nor int3 codes with scales");
@@ -298,13 +362,13 @@ extern "C" int vspec_rocm_attention_cache_host(const float* q, const VspecKVCach
         }
     }
     if (head_dim == 64 || head_dim == 128) {
-        if (tokens > (size_t)INT32_MAX / 2 || heads > (size_t)UINT32_MAX) {
+        if (cache->max_tokens > (size_t)INT32_MAX / 2 || heads > (size_t)UINT32_MAX) {
             vspec_rocm_set_error_("attention: too many tokens");
             return 0;
         }
     } else {
         // other head sizes (the reference demo uses 4) take the generic kernel
-        if (tokens > (size_t)UINT32_MAX || heads > (size_t)UINT32_MAX) {
+        if (cache->max_tokens > (size_t)UINT32_MAX || heads > (size_t)UINT32_MAX) {
             vspec_rocm_set_error_("attention: cache too large");
             return 0;
         }
@@ -313,13 +377,123 @@ extern "C" int vspec_rocm_attention_cache_host(const float* q, const VspecKVCach
             return 0;
         }
     }
-    const size_t kv_bytes = tokens * heads * head_dim * sizeof(float);
-    void *d_k = nullptr, *d_v = nullptr;
-    int ok = hipMalloc(&d_k, kv_bytes) == hipSuccess && hipMalloc(&d_v, kv_bytes) == hipSuccess;
-    if (!ok) vspec_rocm_set_error_("attention: device allocation failed");
-    ok = ok && side_to_device(cache, ks, (float*)d_k) && side_to_device(cache, vs, (float*)d_v) &&
-         attention_rows(q, (const float*)d_k, (const float*)d_v, tokens, heads, head_dim, numerics, out);
-    (void)hipFree(d_k);
-    (void)hipFree(d_v);
-    return ok;
+    std::lock_guard<std::mutex> lock(g_mirror_mu);
+    Mirror* m = mirror_for(cache);
+    if (!m) return 0;
+    // resync from token 0 when the cache shrank or its synced rows changed
+    if (m->synced > tokens || (m->synced && (token_fingerprint(cache, ks, vs, 0) != m->fp_first ||
+                                              token_fingerprint(cache, ks, vs, m->synced - 1) != m->fp_last))) {
+        m->synced = 0;
+    }
+    const size_t t0 = m->synced, n = tokens - t0, H = heads, D = head_dim;
+    const size_t qb = H * D * sizeof(float), row_b = H * D * sizeof(float);
+    // staging layout: q | (start, ctx) | per side: rows (fp32 side) or codes + scales
+    // (int3 side) of the new tokens | per int3 side: decoded rows
+    size_t off_side[2], sz_side[2], off_dec[2];
+    size_t up = align256(qb) + 256;
+    const CacheSide* sides[2] = {&ks, &vs};
+    for (int w = 0; w < 2; ++w) {
+        off_side[w] = up;
+        sz_side[w] = sides[w]->rows ? n * row_b
+                                    : align256(n * H * cache->packed_head_bytes) + n * H * cache->blocks_per_head * sizeof(float);
+        up += align256(sz_side[w]);
+    }
+    size_t dev_total = up;
+    for (int w = 0; w < 2; ++w) {
+        off_dec[w] = dev_total;
+        if (!sides[w]->rows) dev_total += align256(n * row_b);
+    }
+    if (!grow(&m->h_stage, &m->h_stage_bytes, up, true) || !grow(&m->d_stage, &m->stage_bytes, dev_total, false)) {
+        vspec_rocm_set_error_("attention: staging allocation failed");
+        mirror_free(*m);
+        return 0;
+    }
+    uint8_t* hs = m->h_stage;
+    memcpy(hs, q, qb);
+    const int32_t misc[2] = {(int32_t)t0, (int32_t)tokens};
+    memcpy(hs + align256(qb), misc, sizeof(misc));
+    for (int w = 0; w < 2; ++w) {
+        const CacheSide& sd = *sides[w];
+        if (sd.rows) {
+            memcpy(hs + off_side[w], sd.rows + t0 * H * D, n * row_b);
+        } else {
+            memcpy(hs + off_side[w], sd.codes + t0 * H * cache->packed_head_bytes, n * H * cache->packed_head_bytes);
+            memcpy(hs + off_side[w] + align256(n * H * cache->packed_head_bytes), sd.scales + t0 * H * cache->blocks_per_head,
+                   n * H * cache->blocks_per_head * sizeof(float));
+        }
+    }
+    hipStream_t s = nullptr;
+    int ok = hipMemcpyAsync(m->d_stage, hs, up, hipMemcpyHostToDevice, s) == hipSuccess;
+    const float* d_q = (const float*)m->d_stage;
+    const int32_t* d_misc = (const int32_t*)(m->d_stage + align256(qb));
+    const float* new_rows[2];
+    for (int w = 0; ok && w < 2; ++w) {
+        const CacheSide& sd = *sides[w];
+        if (sd.rows) {
+            new_rows[w] = (const float*)(m->d_stage + off_side[w]);
+            continue;
+        }
+        float* dec = (float*)(m->d_stage + off_dec[w]);
+        Int3Rows p = {m->d_stage + off_side[w],
+                      (const float*)(m->d_stage + off_side[w] + align256(n * H * cache->packed_head_bytes)), dec, n * H,
+                      cache->packed_head_bytes, cache->blocks_per_head, (uint32_t)D, (uint32_t)cache->block_size};
+        const size_t elems = n * H * D;
+        if (elems) {
+            const unsigned grid = (unsigned)((elems + kThreads - 1) / kThreads < 8192 ? (elems + kThreads - 1) / kThreads : 8192);
+            hipLaunchKernelGGL(int3_rows_to_f32, dim3(grid), dim3(kThreads), 0, s, p);
+            ok = hipGetLastError() == hipSuccess;
+        }
+        new_rows[w] = dec;
+    }
+    if (!ok) vspec_rocm_set_error_("attention: upload or int3 decode failed");
+    if (ok && m->paged) {
+        const uint32_t nblk = m->kv.num_blocks;
+        ok = vspec_rocm_kv_append(&m->kv, 1, m->d_tab, nblk, d_misc, (uint32_t)n, new_rows[0], new_rows[1], VSPEC_KV_F32, s);
+        if (ok) {
+            VspecPagedAttnDesc d;
+            memset(&d, 0, sizeof(d));
+            d.kv = m->kv;
+            d.batch = 1;
+            d.num_q_heads = (uint32_t)H;
+            d.block_tables = m->d_tab;
+            d.max_blocks_per_seq = nblk;
+            d.ctx_lens = d_misc + 1;
+            d.max_ctx_len = (uint32_t)tokens;
+            d.q = d_q;
+            d.out = m->d_out;
+            d.numerics = numerics;
+            d.stream = s;
+            ok = vspec_rocm_paged_decode_attention(&d);
+        }
+    } else if (ok) {
+        if (n && (hipMemcpyAsync(m->d_k + t0 * H * D, new_rows[0], n * row_b, hipMemcpyDeviceToDevice, s) != hipSuccess ||
+                  hipMemcpyAsync(m->d_v + t0 * H * D, new_rows[1], n * row_b, hipMemcpyDeviceToDevice, s) != hipSuccess)) {
+            vspec_rocm_set_error_("attention: row copy failed");
+            ok = 0;
+        }
+        if (ok) {
+            const bool three = numerics == VSPEC_NUMERICS_3BIT;
+            float scale = 1.0f / sqrtf((float)D);
+            if (three) scale = fminf(fmaxf(scale, 1e-4f), 32.0f);
+            ContigParams p = {d_q, m->d_k, m->d_v, m->d_out, m->d_scores, (uint32_t)tokens, (uint32_t)H, (uint32_t)D,
+                              scale * kLog2e, 4.5f, three ? 24.0f * kLog2e : INFINITY, three ? 16.0f : INFINITY};
+            const size_t smem = (kThreads + D) * sizeof(float);
+            hipLaunchKernelGGL(attention_contig, dim3((unsigned)H), dim3(kThreads), smem, s, p);
+            ok = hipGetLastError() == hipSuccess;
+            if (!ok) vspec_rocm_set_error_("attention: launch failed");
+        }
+    }
+    if (ok && (hipMemcpyAsync(out, m->d_out, qb, hipMemcpyDeviceToHost, s) != hipSuccess ||
+               hipStreamSynchronize(s) != hipSuccess)) {
+        vspec_rocm_set_error_("attention: download failed");
+        ok = 0;
+    }
+    if (!ok) {
+        mirror_free(*m);
+        return 0;
+    }
+    m->synced = tokens;
+    m->fp_first = token_fingerprint(cache, ks, vs, 0);
+    m->fp_last = token_fingerprint(cache, ks, vs, tokens - 1);
+    return 1;
 }
