@@ -228,6 +228,44 @@ __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq
     }
 }
 
+// Work items of one append launch: 2 (K, V) x chunks per row x kv heads x tokens.
+template <int DT>
+__device__ __forceinline__ uint64_t append_items(const AppendParams& p) {
+    return (uint64_t)p.batch * p.n_new * p.hkv * (p.head_dim / append_ept(DT)) * 2;
+}
+
+// One work item of the append kernel (any order; no two items write the same bytes):
+// item `it` = ((token, kv head, chunk) << 1) | which.  Uniform batch (start_pos), packed
+// tokens (token_item / token_pos, items not below n_items skipped) or the decode step's
+// token at ctx_lens[b] - 1.
+template <int DT, int SRC>
+__device__ __forceinline__ void append_item(const AppendParams& p, uint64_t it) {
+    constexpr int EPT = append_ept(DT);
+    const uint32_t chunks = p.head_dim / EPT;
+    const int which = (int)(it & 1);
+    uint64_t r = it >> 1;
+    const uint32_t c = (uint32_t)(r % chunks);
+    r /= chunks;
+    const uint32_t h = (uint32_t)(r % p.hkv);
+    r /= p.hkv;
+    const uint32_t i = (uint32_t)(r % p.n_new);
+    const uint32_t b = (uint32_t)(r / p.n_new);
+
+    const int32_t item = p.token_item ? p.token_item[b] : (int32_t)b;
+    int32_t sp;
+    if (p.token_item) {
+        sp = p.token_pos[b];
+    } else if (p.start_pos) {
+        sp = p.start_pos[b];
+    } else {
+        const int32_t cl = p.ctx_lens[b];
+        sp = cl > 0 ? cl - 1 : -1;
+    }
+    if (sp < 0 || item < 0 || (p.token_item && (uint32_t)item >= p.n_items)) return;
+    const size_t src_el = (((size_t)b * p.n_new + i) * p.hkv + h) * p.head_dim + (size_t)c * EPT;
+    append_chunk<DT, SRC>(p, (uint32_t)item, (uint32_t)sp + i, h, c, which, src_el);
+}
+
 // Fused decode-step append of the MFMA decode kernels (p.k_new != null).  Every work
 // item whose last tile lies in this workgroup's range [ws.lo, ws.hi) -- exactly one
 // workgroup per work item -- gets its sequence's new token written for its kv head at

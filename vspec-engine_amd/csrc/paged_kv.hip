@@ -366,33 +366,10 @@ __global__ __launch_bounds__(D) void decode_combine(DecodeParams p) {
 // 32-element quantisation group for int4 pools, 8 elements (16 or 32 bytes) otherwise.
 template <int DT, int SRC>
 __global__ __launch_bounds__(256) void kv_append(AppendParams p) {
-    constexpr int EPT = append_ept(DT);
-    const uint32_t chunks = p.head_dim / EPT;
-    const uint64_t total = (uint64_t)p.batch * p.n_new * p.hkv * chunks * 2;
+    const uint64_t total = append_items<DT>(p);
     for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
          it += (uint64_t)gridDim.x * blockDim.x) {
-        const int which = (int)(it & 1);
-        uint64_t r = it >> 1;
-        const uint32_t c = (uint32_t)(r % chunks);
-        r /= chunks;
-        const uint32_t h = (uint32_t)(r % p.hkv);
-        r /= p.hkv;
-        const uint32_t i = (uint32_t)(r % p.n_new);
-        const uint32_t b = (uint32_t)(r / p.n_new);
-
-        const int32_t item = p.token_item ? p.token_item[b] : (int32_t)b;
-        int32_t sp;
-        if (p.token_item) {
-            sp = p.token_pos[b];
-        } else if (p.start_pos) {
-            sp = p.start_pos[b];
-        } else {
-            const int32_t cl = p.ctx_lens[b];
-            sp = cl > 0 ? cl - 1 : -1;
-        }
-        if (sp < 0 || item < 0 || (p.token_item && (uint32_t)item >= p.n_items)) continue;
-        const size_t src_el = (((size_t)b * p.n_new + i) * p.hkv + h) * p.head_dim + (size_t)c * EPT;
-        append_chunk<DT, SRC>(p, (uint32_t)item, (uint32_t)sp + i, h, c, which, src_el);
+        append_item<DT, SRC>(p, it);
     }
 }
 
