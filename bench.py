@@ -543,8 +543,10 @@ def main():
     k_new = torch.randn((B, 1, Hkv, D), generator=g, device=dev, dtype=torch.float16)
     v_new = torch.randn((B, 1, Hkv, D), generator=g, device=dev, dtype=torch.float16)
     out = torch.empty_like(q)
-    descs = [vr.make_decode_desc(pools[c], tables_l[c], ctx, q, out, T, mode,
-                                 partition_tokens=args.partition_tokens) for c in range(copies)]
+    # the host knows the contexts: min_ctx_len lets a uniform batch skip the merge launch
+    # when no work item spans two workgroups
+    descs = [vr.make_decode_desc(pools[c], tables_l[c], ctx, q, out, T, mode, partition_tokens=args.partition_tokens,
+                                 min_ctx_len=min(lens)) for c in range(copies)]
     ws_bytes = max(vr.decode_workspace_bytes(d) for d in descs)
     ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
     import ctypes as C

@@ -140,6 +140,11 @@ typedef struct VspecPagedAttnDesc {
      * used count are skipped.  The decode step appends at span - 1.  NULL: every block is
      * full except the last, and ctx_lens[b] is the token count. */
     const int32_t* block_used;
+    /* Optional host lower bound of ctx_lens (0: none).  When it equals max_ctx_len (every
+     * context the same) the host knows the work split exactly and skips the merge launch
+     * if no work item spans two workgroups (e.g. 64 x 4097 tokens on 256 CUs).  A context
+     * below a non-zero bound is a caller error (its output may be left unwritten). */
+    uint32_t min_ctx_len;
 } VspecPagedAttnDesc;
 
 size_t vspec_rocm_paged_decode_workspace_bytes(const VspecPagedAttnDesc* desc);

@@ -867,6 +867,47 @@ def test_decode_step_new_token_dominates(oracle, gpu, flag_gate, dtype):
     check_attention(oracle, full, got, 1)
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
+@pytest.mark.parametrize("B,T,pt", [(64, 4097, 0), (16, 2049, 0), (3, 300, 0), (8, 1025, 32), (8, 1024, 64)])
+def test_decode_min_ctx_len_hint(gpu, dtype, B, T, pt):
+    """min_ctx_len == max_ctx_len (every context the same) lets the host skip the merge
+    launch when no work item spans two workgroups (64 x 4097: each workgroup holds whole
+    items) and keeps it otherwise; the decode step's outputs and pool bytes equal those
+    without the hint bit for bit, with the balanced and the chunked split."""
+    import ctypes as C
+
+    import torch
+    import vspec_rocm as vr
+
+    say(f"[min_ctx_len] dtype={dtype} B={B} T={T} pt={pt}")
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    nblk = (T + P - 1) // P
+    g = torch.Generator(device=gpu)
+    g.manual_seed(B * 131 + T + dtype)
+    pools = [vr.PagedPool(dtype, B * nblk, P, Hkv, D, device=gpu) for _ in range(2)]
+    tab = torch.randperm(B * nblk, generator=g, device=gpu).to(torch.int32).view(B, nblk).contiguous()
+    kk = torch.randn((B, T - 1, Hkv, D), generator=g, device=gpu, dtype=torch.float16)
+    vv = torch.randn((B, T - 1, Hkv, D), generator=g, device=gpu, dtype=torch.float16)
+    for pl in pools:
+        vr.kv_append(pl, tab, torch.zeros(B, dtype=torch.int32, device=gpu), kk, vv)
+    ctx = torch.full((B,), T, dtype=torch.int32, device=gpu)
+    q = torch.randn((B, Hq, D), generator=g, device=gpu)
+    kn = torch.randn((B, Hkv, D), generator=g, device=gpu, dtype=torch.float16)
+    vn = torch.randn((B, Hkv, D), generator=g, device=gpu, dtype=torch.float16)
+    outs = []
+    for i, hint in enumerate((0, T)):
+        out = torch.full_like(q, float("nan"))
+        d = vr.make_decode_desc(pools[i], tab, ctx, q, out, T, vr.NUMERICS_3BIT, partition_tokens=pt, min_ctx_len=hint)
+        assert vr.lib().vspec_rocm_paged_decode_step(C.byref(d), kn.data_ptr(), vn.data_ptr(), vr.KV_F16), vr.last_error()
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0]).all()
+    assert torch.equal(outs[0], outs[1])
+    for a, b in zip(pool_bytes(pools[0]), pool_bytes(pools[1])):
+        if a is not None:
+            assert np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+
+
 def test_graph_replay_survives_workspace_growth(oracle, gpu):
     """A decode captured into a HIP graph with the library's own workspace; then an eager
     decode on the same stream that needs a larger workspace makes the library replace it.

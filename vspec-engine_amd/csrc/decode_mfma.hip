@@ -457,8 +457,10 @@ void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
     if (p.block_used) launch_used<D, GW, true>(p, grid, s);
     else launch_used<D, GW, false>(p, grid, s);
     // items split over several workgroups (same split: the f16 kernel's pair shares)
-    const dim3 merge_grid(p.batch * p.hkv * p.gsplit);
-    hipLaunchKernelGGL((decode_merge_split<D, GW, true>), merge_grid, dim3(kWaves * 64), 0, s, p);
+    if (p.merge) {
+        const dim3 merge_grid(p.batch * p.hkv * p.gsplit);
+        hipLaunchKernelGGL((decode_merge_split<D, GW, true>), merge_grid, dim3(kWaves * 64), 0, s, p);
+    }
 }
 
 template <int D>

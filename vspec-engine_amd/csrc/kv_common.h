@@ -207,6 +207,7 @@ struct DecodeParams {
     // split of the MFMA kernels (see WorkSplit): part_ml / part_acc then hold two
     // partial slots per workgroup, [grid][2][GW][2] and [grid][2][GW][D]
     uint32_t split_grid;   // workgroups of the split kernel's grid (the merge launch redoes the split)
+    bool merge;            // the host could not rule out work items spanning two workgroups
     uint32_t batch;
     uint32_t max_tiles;    // tiles of the host's context bound (max_ctx_len)
     uint32_t chunk_tiles;  // tiles per workgroup, or 0: split evenly over gridDim.x

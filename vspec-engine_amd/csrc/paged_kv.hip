@@ -793,6 +793,7 @@ uint32_t decode_flag_min_tiles() {
 }
 
 struct DecodePlan {
+    bool merge;  // split MFMA kernels: some work item may span two workgroups (merge launch)
     uint32_t gw;
     uint32_t gsplit;
     uint32_t tiles_per_part;
@@ -807,7 +808,33 @@ struct DecodePlan {
     uint32_t max_tiles;
 };
 
+// With every context known to be the same (min_ctx_len == the context bound), the split
+// of the MFMA kernels (kv_common.h work_split with equal shares, as for any batch whose
+// contexts are equal) is known on the host: returns whether some range boundary falls
+// strictly inside a work item.  Without that knowledge a merge launch is always needed.
+bool uniform_split_has_partials(const VspecPagedAttnDesc* d, const DecodePlan* pl, uint64_t ctx_bound) {
+    if (!d->min_ctx_len || d->min_ctx_len < ctx_bound) return true;
+    const uint64_t items = (uint64_t)d->batch * d->kv.num_kv_heads * pl->gsplit;
+    const uint64_t ctx = ctx_bound < (uint64_t)d->max_blocks_per_seq * d->kv.block_tokens
+                             ? ctx_bound : (uint64_t)d->max_blocks_per_seq * d->kv.block_tokens;
+    uint64_t U = (ctx + kTile - 1) / kTile;
+    if (U > pl->max_tiles) U = pl->max_tiles;
+    if (U < 1) U = 1;
+    const uint64_t T = items * U;
+    if (pl->chunk_tiles) return pl->chunk_tiles % U != 0 && T > pl->chunk_tiles;
+    uint64_t G = pl->grid_x < T ? pl->grid_x : T;
+    if (pl->min_tiles > 1) {
+        const uint64_t cap = T / pl->min_tiles > 1 ? T / pl->min_tiles : 1;
+        if (cap < G) G = cap;
+    }
+    for (uint64_t g = 1; g < G; ++g) {
+        if ((g * T / G) % U != 0) return true;
+    }
+    return false;
+}
+
 int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
+    pl->merge = true;
     const uint32_t hkv = d->kv.num_kv_heads;
     if (d->num_q_heads == 0 || d->num_q_heads % hkv != 0) {
         set_err("paged_decode: num_q_heads must be a positive multiple of num_kv_heads");
@@ -867,6 +894,9 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
         pl->max_tiles = max_tiles;
         pl->tiles_per_part = 0;
         pl->max_parts = 1;
+        pl->merge = uniform_split_has_partials(d, pl, ctx_bound);
+        // the workspace stays even without a merge launch: a context below min_ctx_len (a
+        // caller error) then leaves its partial states in valid memory, not its output
         pl->ws_bytes = (size_t)pl->grid_x * 2 * pl->gw * (2 + d->kv.head_dim) * sizeof(float);
         return 1;
     }
@@ -1362,6 +1392,7 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.logit_clip = three ? 24.0f * kLog2e : INFINITY;
     p.input_clip = three ? 16.0f : INFINITY;
     p.split_grid = pl.split ? pl.grid_x : 0u;
+    p.merge = pl.split && pl.merge;
     p.batch = desc->batch;
     p.max_tiles = pl.max_tiles;
     p.chunk_tiles = pl.chunk_tiles;

@@ -58,6 +58,7 @@ class VspecPagedAttnDesc(C.Structure):
         ("workspace_bytes", C.c_size_t),
         ("stream", _vp),
         ("block_used", _vp),
+        ("min_ctx_len", C.c_uint32),
     ]
 
 
@@ -437,7 +438,7 @@ def kv_compact(pool: PagedPool, src_blocks, dst_blocks, stream=None):
 
 def make_decode_desc(pool: PagedPool, block_tables, ctx_lens, q, out, max_ctx_len, numerics=NUMERICS_PLAIN,
                      scale=0.0, partition_tokens=0, workspace=None, stream=None,
-                     block_used=None) -> VspecPagedAttnDesc:
+                     block_used=None, min_ctx_len=0) -> VspecPagedAttnDesc:
     B, Hq, D = q.shape
     d = VspecPagedAttnDesc()
     d.kv = pool.desc()
@@ -451,6 +452,7 @@ def make_decode_desc(pool: PagedPool, block_tables, ctx_lens, q, out, max_ctx_le
         d.workspace, d.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     d.stream = _stream(stream)
     d.block_used = _ptr(block_used)
+    d.min_ctx_len = min_ctx_len
     return d
 
 
