@@ -63,26 +63,72 @@ struct I4Frags {
     uint32_t fword;       // index of that flag word (wave-uniform)
 };
 
-// fp16 number i of a packed array, as the f16 operand of a mixed-precision FMA
-__device__ __forceinline__ _Float16 half_at(const uint32_t* w, int i) {
-    return __builtin_bit_cast(h2_t, w[i >> 1])[i & 1];
+// ---- tile loads straight into LDS (buffer_load ... lds) ----
+//
+// A wave's next tile pairs stream into an LDS ring while it works on the current pair
+// from registers, so the loads in flight take no VGPRs.  Each load goes through a buffer
+// descriptor bounded to the tile's bytes (out-of-range lanes and descriptors of size 0
+// write zeros and read nothing), built on the scalar unit per tile; the per-lane offsets
+// are loop invariants.  Lane i of a load writes its bytes at M0 + size * i.
+//
+// The loads are issued from inline asm (a compiler-visible LDS DMA makes every later LDS
+// read wait for all of them), so their waits are explicit: vector memory operations
+// complete in issue order, and s_waitcnt vmcnt(n) returns once at most n are in flight,
+// so waiting for (pairs in flight - 1) x 8 loads lands the oldest pair.  Loads the
+// compiler issues itself in between could only make such a wait longer.
+typedef int32_t rsrc_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    // word 1: base bits 32..47, stride 0; word 3: 32-bit data format (raw buffer access)
+    return rsrc_t{(int32_t)(uint32_t)a, (int32_t)((uint32_t)(a >> 32) & 0xffffu), (int32_t)bytes, 0x00020000};
 }
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)reinterpret_cast<uintptr_t>(p); }
+// 16 (4) bytes per lane from the descriptor's base + voff into LDS at lds + 16 (4) * lane
+__device__ __forceinline__ void lds_load16(uint32_t lds, rsrc_t r, uint32_t voff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen nt lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_load4(uint32_t lds, rsrc_t r, uint32_t voff) {
+    asm volatile("buffer_load_dword %0, %1, 0 offen nt lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// LDS reads done (before a load overwrites what they read)
+__device__ __forceinline__ void wait_lds_reads() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// One tile pair of a wave in LDS: codes and scales of tiles a and b.  K and V codes are
+// stored so that lane (g, n) finds its operand chunk at 16 * lane (D = 128) or at the
+// chunk's offset in the tile (D = 64); the scales as in the pools, K [group][16 tokens]
+// then V [16 tokens][group] (fp16), loaded by lanes 0..31 only (at most 128 bytes each).
+struct I4Stage {
+    uint4 k[2][64];
+    uint4 v[2][64];
+    uint32_t sc[2][64];  // [0, 32): K scales, [32, 64): V scales
+};
+constexpr int kLoadsPerPair = 8;  // LDS loads per tile pair (K, V, K scales, V scales per tile)
 
 #ifndef VSPEC_I4_MIN_WG_PER_CU
 #define VSPEC_I4_MIN_WG_PER_CU 2
 #endif
 
-// FL: the tile loop takes the pool's clamp flags (and screens only what they cannot say);
-// without FL it screens every tile, a lighter loop for short per-workgroup shares.
-// USED: per-block used counts cap each tile (block_used).
-template <int D, int GW, int PB, int NB, bool FL, bool USED>
+// ST: tile pairs in flight per wave (LDS stages); FL: the tile loop takes the pool's clamp
+// flags (and screens only what they cannot say); without FL it screens every tile, a
+// lighter loop for short per-workgroup shares.  USED: per-block used counts cap each tile
+// (block_used).
+template <int D, int GW, int PB, int ST, bool FL, bool USED>
 __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(DecodeParams p) {
     constexpr int NQ = D / 32;   // code dwords per lane = QK MFMAs per tile = groups
     constexpr int NG = D / 32;
     constexpr int NDT = D / 16;  // PV d-tiles
+    __shared__ I4Stage stg[ST][kWaves];
+    // the waves' softmax states at the end of a work item, in the ring's memory (between
+    // the barrier after the tile loops and the one before the next item's loads)
+    static_assert(sizeof(float) * kWaves * GW * (D + 2) <= sizeof(stg), "wave states fit the ring");
+    float(*comb)[GW][D + 2] = reinterpret_cast<float(*)[GW][D + 2]>(&stg[0][0]);
     __shared__ float qs[GW][D];
     __shared__ uint4 qb_lds[NQ][2][64];  // QK B operands (hi, lo) per lane
-    __shared__ float comb[kWaves][GW][D + 2];
     __shared__ float patch_val[kWaves][kTile][4];
     __shared__ int patch_flag[kWaves][kTile];
     __shared__ SplitShared split_sh;
@@ -126,6 +172,110 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         const int hq0 = hk * ((int)p.gsplit * GW) + (y % (int)p.gsplit) * GW;
         const int ctx = min(max(as_const(p.ctx_lens)[b], 0), (int)(p.max_blocks * p.block_tokens));
 
+        const int P = PB ? PB : (int)p.block_tokens;
+        const int tiles_per_block = P / kTile;
+        const const_i32* table = as_const(p.block_tables) + (size_t)b * p.max_blocks;
+        const const_i32* used_row = USED ? as_const(p.block_used) + (size_t)b * p.max_blocks : nullptr;
+        const int own_group = (g * NQ) >> 2;
+        const int col_group = (n >> 2) % NG;
+
+        // clamp flags from the pool (see screen below); `fused`: this launch appended each
+        // work item's last token
+        const bool flags_on = FL && p.alpha >= 4.5f;
+        const bool fused = p.k_new != nullptr;
+        auto valid_mask = [](int nvalid) -> uint32_t { return nvalid >= kTile ? 0xffffu : (1u << nvalid) - 1u; };
+
+        // ---- tile pairs into this wave's LDS ring ----
+        // Per-lane byte offsets of the loads: K lane (g, n) takes token n's code dwords
+        // g*NQ.. (D = 128: 16 bytes, stored lane-major; D = 64: the tile's 512 bytes copied
+        // by lanes 0-31); V tiles are lane-major chunks already; the K scales' NG rows of 16
+        // tokens (row stride P) and the V scales' 16 x NG go one dword per lane.
+        const uint32_t off_k = NQ == 4 ? (uint32_t)(n * (D / 2) + 16 * g) : 16u * (uint32_t)lane;
+        const uint32_t off_v = 16u * (uint32_t)lane;
+        const uint32_t off_ks = lane < 8 * NG ? (uint32_t)((lane >> 3) * P * 2 + 4 * (lane & 7)) : 0x40000000u;
+        static_assert(8 * NG <= 32, "the scales of a tile fit lanes 0..31");
+        const uint32_t off_vs = 4u * (uint32_t)lane;
+        // per stage: how many of each tile's tokens its block holds (16, or block_used's
+        // cap; 0: none), its clamp flag word and that word's index (all wave-uniform)
+        int cap_s[ST][2];
+        uint32_t flag_s[ST][2], fword_s[ST][2];
+        // Table entries (and used counts) of a pair's tiles, read one pair ahead of its loads
+        // so that the scalar reads are not waited for on the way to the loads.  The tile
+        // index is wave-uniform, so the table, used-count and flag reads stay on the scalar
+        // unit.
+        struct Look {
+            int entry[2];
+            int used[2];
+        };
+        auto lookup = [&](int tile_a) -> Look {
+            Look l;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int tile = __builtin_amdgcn_readfirstlane(tile_a + h);
+                const int entry_idx = (tile < tile_end ? tile : tile_end - 1) / tiles_per_block;
+                l.entry[h] = table[entry_idx];
+                l.used[h] = USED ? used_row[entry_idx] : kTile;
+            }
+            return l;
+        };
+        // The loads of one tile.  A tile past the range or behind an invalid table entry gets
+        // descriptors of size 0 (zeros, no memory traffic) and cap 0.
+        auto issue_tile = [&](int tile, const int entry, const int used, I4Stage& st, const int h, int& cap,
+                              uint32_t& flag, uint32_t& fword) {
+            tile = __builtin_amdgcn_readfirstlane(tile);
+            const bool ok = tile < tile_end && entry >= 0 && (uint32_t)entry < p.num_blocks;
+            const size_t bh = (size_t)(ok ? entry : 0) * p.hkv + hk;
+            const int slot0 = (tile % tiles_per_block) * kTile;
+            const uint32_t code_bytes = ok ? 8u * D : 0u;
+            lds_load16(lds_addr(&st.k[h][0]), tile_rsrc(p.k + (bh * P + slot0) * (D / 2), code_bytes), off_k);
+            lds_load16(lds_addr(&st.v[h][0]),
+                       tile_rsrc(p.v + bh * ((size_t)P * D / 2) + (size_t)(slot0 / kTile) * (8 * D), code_bytes), off_v);
+            if (lane < 32) {
+                lds_load4(lds_addr(&st.sc[h][0]),
+                          tile_rsrc(p.ks + bh * NG * P + slot0, ok ? (uint32_t)(((NG - 1) * P + kTile) * 2) : 0u), off_ks);
+                lds_load4(lds_addr(&st.sc[h][32]), tile_rsrc(p.vs + (bh * P + slot0) * NG, ok ? 32u * NG : 0u), off_vs);
+            }
+            fword = (uint32_t)(bh * (P / kTile) + slot0 / kTile);
+            flag = flags_on ? (uint32_t)as_const(reinterpret_cast<const int32_t*>(p.kf))[fword] : 0u;
+            if constexpr (USED) cap = ok ? used_cap(used, slot0) : 0;
+            else cap = ok ? kTile : 0;
+        };
+        auto issue = [&](int tile_a, int u, const Look& l) {
+            issue_tile(tile_a, l.entry[0], l.used[0], stg[u][wave], 0, cap_s[u][0], flag_s[u][0], fword_s[u][0]);
+            issue_tile(tile_a + 1, l.entry[1], l.used[1], stg[u][wave], 1, cap_s[u][1], flag_s[u][1], fword_s[u][1]);
+        };
+        // a stage's tile h into registers: the K half (codes, K scales) and the V half
+        auto fetch_k = [&](const I4Stage& st, const int h, I4Frags<D>& f) {
+            if constexpr (NQ == 4) {
+                const uint4 a = st.k[h][lane];
+                f.k[0] = a.x; f.k[1] = a.y; f.k[2] = a.z; f.k[3] = a.w;
+            } else {
+                const uint2 a = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(&st.k[h][0]) + n * (D / 2) + 8 * g);
+                f.k[0] = a.x; f.k[1] = a.y;
+            }
+            const uint8_t* ks = reinterpret_cast<const uint8_t*>(&st.sc[h][0]);
+            f.ks_own = *reinterpret_cast<const uint16_t*>(ks + own_group * 32 + 2 * n);
+            f.ks_col = *reinterpret_cast<const uint2*>(ks + col_group * 32 + 8 * g);
+        };
+        auto fetch_v = [&](const I4Stage& st, const int h, I4Frags<D>& f) {
+            if constexpr (NQ == 4) {
+                const uint4 c = st.v[h][lane];
+                f.v[0] = c.x; f.v[1] = c.y; f.v[2] = c.z; f.v[3] = c.w;
+            } else {
+                const uint2 c = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(&st.v[h][0]) + 8 * lane);
+                f.v[0] = c.x; f.v[1] = c.y;
+            }
+            const uint4* vs = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(&st.sc[h][32]) + 8 * NG * g);
+#pragma unroll
+            for (int i = 0; i < NQ / 2; ++i) {
+                const uint4 w = vs[i];
+                f.vs[4 * i] = w.x; f.vs[4 * i + 1] = w.y; f.vs[4 * i + 2] = w.z; f.vs[4 * i + 3] = w.w;
+            }
+        };
+
+        const int step = 2 * kWaves;
+        const int t0 = tile_begin + 2 * wave;
+
         // ---- q' = clip(q) * scale * log2(e): wave w prepares head w ----
         if (wave < GW) {
             const float* qrow = p.q + ((size_t)b * p.hq + hq0 + wave) * D;
@@ -149,6 +299,11 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 #pragma unroll
             for (int e = 0; e < E; ++e) qs[wave][lane * E + e] = fminf(fmaxf(x[e], -th), th) * p.qscale;
         }
+        // the first ST pairs are on their way while the q operands are prepared (after the
+        // q rows are in registers: a wait for those would also wait for these)
+#pragma unroll
+        for (int u = 0; u < ST; ++u) issue(t0 + u * step, u, lookup(t0 + u * step));
+        Look next = lookup(t0 + ST * step);
         __syncthreads();
 
         // ---- QK B operands: k-slots 8g..8g+7 of MFMA m carry code dword dw = g*NQ + m in
@@ -174,74 +329,18 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         }
         __syncthreads();
 
-        const int P = PB ? PB : (int)p.block_tokens;
-        const int tiles_per_block = P / kTile;
-        const const_i32* table = as_const(p.block_tables) + (size_t)b * p.max_blocks;
-        const const_i32* used_row = USED ? as_const(p.block_used) + (size_t)b * p.max_blocks : nullptr;
-        const int own_group = (g * NQ) >> 2;
-        const int col_group = (n >> 2) % NG;
-
-        // clamp flags from the pool (see screen below); `fused`: this launch appended each
-        // work item's last token
-        const bool flags_on = FL && p.alpha >= 4.5f;
-        const bool fused = p.k_new != nullptr;
-        auto valid_mask = [](int nvalid) -> uint32_t { return nvalid >= kTile ? 0xffffu : (1u << nvalid) - 1u; };
-
-        // Loads are issued unconditionally (a tile past the range or behind an invalid
-        // table entry reads block 0 and holds no valid token): with no branches around
-        // them the compiler counts outstanding loads exactly and waits only for the tile
-        // it needs.  The tile index is wave-uniform, so the table read stays on the scalar
-        // unit.  Returns how many of the tile's tokens its block holds (16, or
-        // block_used's cap; 0: none).
-        auto load = [&](int tile, I4Frags<D>& f) -> int {
-            tile = __builtin_amdgcn_readfirstlane(tile);
-            const bool in_range = tile < tile_end;
-            const int entry_idx = (in_range ? tile : tile_end - 1) / tiles_per_block;
-            const int entry = table[entry_idx];
-            const bool ok = in_range && entry >= 0 && (uint32_t)entry < p.num_blocks;
-            const int phys = ok ? entry : 0;
-            const size_t bh = (size_t)phys * p.hkv + hk;
-            const int slot0 = (tile % tiles_per_block) * kTile;
-            const uint8_t* kr = p.k + (bh * P + slot0 + n) * (D / 2) + 4 * g * NQ;
-            const uint8_t* vc = p.v + bh * ((size_t)P * D / 2) + (size_t)(slot0 / kTile) * (8 * D) + (16 * g + n) * (D / 8);
-            if constexpr (NQ == 4) {
-                const uint4 a = load_stream4(kr);
-                const uint4 c = load_stream4(vc);
-                f.k[0] = a.x; f.k[1] = a.y; f.k[2] = a.z; f.k[3] = a.w;
-                f.v[0] = c.x; f.v[1] = c.y; f.v[2] = c.z; f.v[3] = c.w;
-            } else {
-                const uint2 a = load_stream2(kr);
-                const uint2 c = load_stream2(vc);
-                f.k[0] = a.x; f.k[1] = a.y;
-                f.v[0] = c.x; f.v[1] = c.y;
-            }
-            f.ks_own = load_stream_u16(p.ks + (bh * NG + own_group) * P + slot0 + n);
-            f.ks_col = load_stream2(p.ks + (bh * NG + col_group) * P + slot0 + 4 * g);
-            // a vector load, waited for with the tile's other loads (a scalar load would be
-            // waited for by every LDS wait of the loop: the two share a counter)
-            f.fword = (uint32_t)(bh * (P / kTile) + slot0 / kTile);
-            f.flags = flags_on ? __hip_atomic_load(p.kf + f.fword, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) : 0u;
-            const uint4* vs = reinterpret_cast<const uint4*>(p.vs + (bh * P + slot0 + 4 * g) * NG);
-#pragma unroll
-            for (int i = 0; i < NQ / 2; ++i) {
-                const uint4 w = load_stream4(vs + i);
-                f.vs[4 * i] = w.x; f.vs[4 * i + 1] = w.y; f.vs[4 * i + 2] = w.z; f.vs[4 * i + 3] = w.w;
-            }
-            if constexpr (USED) return ok ? used_cap(used_row[entry_idx], slot0) : 0;
-            return ok ? kTile : 0;
-        };
-
-        // score clip per lane: columns that hold no head clip to -inf (3-bit mode: +-24*log2e)
-        const float clip_hi = n < GW ? p.logit_clip : -INFINITY;
-        const float clip_lo = n < GW ? -p.logit_clip : -INFINITY;
-
         f4_t acc[NDT];
 #pragma unroll
         for (int j = 0; j < NDT; ++j) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
-        // running max starts finite so exp2(s - m_run) is 0, never NaN, in the columns
-        // that hold no head (their scores stay -inf)
-        float m_run = -1e30f;
+        // Online softmax state.  Scores are formed relative to the running max m_run
+        // (the K-scale FMA subtracts it), so the score clip moves with it: clip_lo/hi hold
+        // the clip bounds minus m_run; columns that hold no head clip to -inf (3-bit mode:
+        // +-24*log2e).  The wave's first scored pair of a work item sets m_run outright.
+        float m_run = 0.f;
         float l_run = 0.f;
+        float clip_hi = n < GW ? p.logit_clip : -INFINITY;
+        float clip_lo = n < GW ? -p.logit_clip : -INFINITY;
+        bool first = true;
 
         // Clamp screen of key n of a tile (this lane: one group's codes): mean and E[x^2]
         // from integer code sums; this group's |x| <= 8 * scale.  `flag` is set in a lane
@@ -274,24 +373,27 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // keys (bit n) with a flagged lane, from a wave ballot
         auto tokens = [](uint64_t m) -> uint32_t { return (uint32_t)((m | (m >> 16) | (m >> 32) | (m >> 48)) & 0xffffu); };
 
-        // Scores of a tile on the matrix cores: lane (g, n) gets tokens 4g..4g+3 for head
-        // n%4 (hi and lo products accumulate in separate chains).
+        // Scores of a tile on the matrix cores, minus m_run: lane (g, n) gets tokens
+        // 4g..4g+3 for head n%4.  The hi and lo products accumulate in one chain (the lo
+        // part is 2^-11 of the hi part: one fp32 accumulator keeps both); each of the four
+        // group columns of a head is scaled by its fp16 K scale and takes a quarter of
+        // m_run in the same mixed-precision FMA, so the column sum is score - m_run.
         auto qk = [&](const I4Frags<D>& f) -> f4_t {
-            f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+            f4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int m = 0; m < NQ; ++m) {
                 uint32_t pr4[4];
                 codes_to_f16(f.k[m], pr4);
                 const h8_t a = __builtin_bit_cast(h8_t, make_uint4(pr4[0], pr4[1], pr4[2], pr4[3]));
-                sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, qb_lds[m][0][lane]), sh, 0, 0, 0);
-                sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, qb_lds[m][1][lane]), sl, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, qb_lds[m][0][lane]), sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, qb_lds[m][1][lane]), sacc, 0, 0, 0);
             }
-            const uint32_t kc[2] = {f.ks_col.x, f.ks_col.y};
+            const h2_t kc[2] = {__builtin_bit_cast(h2_t, f.ks_col.x), __builtin_bit_cast(h2_t, f.ks_col.y)};
+            const float mq = -0.25f * m_run;
             f4_t sc;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float ks = (float)half_at(kc, r);
-                float v = __builtin_fmaf(sh[r], ks, sl[r] * ks);
+                float v = __builtin_fmaf(sacc[r], (float)kc[r >> 1][r & 1], mq);
                 v += row_dpp<kRowRor8>(v);
                 v += row_dpp<kRowRor4>(v);
                 sc[r] = v;
@@ -338,7 +440,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int t = 4 * g + r;
-                    if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n];
+                    if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n] - m_run;
                 }
             }
         };
@@ -359,9 +461,9 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 
         // Two tiles per step: k-slot 8g + i of the PV MFMA is token 4g + i of tile A (i < 4)
         // or token 4g + i - 4 of tile B.
-        auto process = [&](I4Frags<D>& fa, I4Frags<D>& fb, const int capa, const int capb, const int tile_a) {
-            const int nva = max(0, min(capa, ctx - tile_a * kTile));
-            const int nvb = max(0, min(capb, ctx - (tile_a + 1) * kTile));
+        // Scores and softmax weights of a pair (the V half of the fragments is not read yet).
+        auto scores = [&](I4Frags<D>& fa, I4Frags<D>& fb, const int nva, const int nvb, const int tile_a,
+                          float (&pr)[8]) {
             // clamp flags: from the pool, or from the screen (both tiles in one basic block:
             // their chains interleave)
             // the tile this launch appended into: its word with the appended key's flag
@@ -392,9 +494,10 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 if (flb != 0u) exact(fb, flb, sb);
             }
 
-            // ---- online softmax for head n over this lane's 8 tokens.  The running max
-            // moves only when a score exceeds it by more than 8 (p stays <= 2^8), so the
-            // cross-lane max is taken only then. ----
+            // ---- online softmax for head n over this lane's 8 tokens (scores relative to
+            // m_run).  The running max moves only when a score exceeds it by more than 8
+            // (p stays <= 2^8), so the cross-lane max is taken only then, and on the first
+            // scored pair. ----
             float s[8];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -411,23 +514,36 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             float smax = s[0];
 #pragma unroll
             for (int i = 1; i < 8; ++i) smax = fmaxf(smax, s[i]);
-            const bool over = smax > m_run + 8.0f;
-            if (__builtin_amdgcn_ballot_w64(over) != 0) {
+            if (first || __builtin_amdgcn_ballot_w64(smax > 8.0f) != 0) {
                 const float mt = max_rows(smax);
-                const bool need = mt > m_run + 8.0f;
-                const float fct = need ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
-                m_run = need ? mt : m_run;
+                // columns without a head (all -inf) contribute no move; the four group
+                // columns of a head (lanes n, n+4, n+8, n+12: each subtracts a quarter of
+                // its own m_run in qk) all take the head's move
+                const bool need = first ? mt > -INFINITY : mt > 8.0f;
+                float dm = need ? mt : 0.0f;
+                dm += row_dpp<kRowRor8>(dm);
+                dm += row_dpp<kRowRor4>(dm);
+                const float fct = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
+                m_run += dm;
+                clip_lo -= dm;
+                clip_hi -= dm;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s[i] -= dm;
                 l_run *= fct;
 #pragma unroll
                 for (int j = 0; j < NDT; ++j) acc[j] *= fct;
             }
+            if (nva > 0 || nvb > 0) first = false;
             // v_exp_f32 of -inf is +0: masked tokens and unused columns drop out
-            float pr[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                pr[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
+                pr[i] = __builtin_amdgcn_exp2f(s[i]);
                 l_run += pr[i];
             }
+        };
+
+        // O^T += V^T P'^T for a pair whose V half of the fragments is in registers
+        auto pv = [&](I4Frags<D>& fa, I4Frags<D>& fb, const int nva, const int nvb, const float (&pr)[8]) {
             clear_masked_scales(fa, nva);
             clear_masked_scales(fb, nvb);
 
@@ -439,8 +555,9 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 h8_t pq;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const _Float16 sv = i < 4 ? half_at(fa.vs, (i & 3) * NG + q) : half_at(fb.vs, (i & 3) * NG + q);
-                    pq[i] = (_Float16)__builtin_fmaf(pr[i], (float)sv, 0.0f);
+                    const int k = (i & 3) * NG + q;
+                    const h2_t v2 = __builtin_bit_cast(h2_t, i < 4 ? fa.vs[k >> 1] : fb.vs[k >> 1]);
+                    pq[i] = (_Float16)__builtin_fmaf(pr[i], (float)v2[k & 1], 0.0f);
                 }
                 uint32_t ka[4], kb[4];
                 codes_to_f16(fa.v[q], ka);
@@ -452,29 +569,41 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             }
         };
 
-        // Pairs of consecutive tiles; NB pairs in flight per wave.  Pair i (from the
-        // partition start) is tiles tile_begin + 2i, +1; wave w takes i = w, w + kWaves, ...
-        I4Frags<D> fa[NB], fb[NB];
-        int oka[NB], okb[NB];
-        const int step = 2 * kWaves;
-        const int t0 = tile_begin + 2 * wave;
+        for (int tile = t0; tile < tile_end; tile += ST * step) {
 #pragma unroll
-        for (int u = 0; u < NB; ++u) {
-            const int t = t0 + u * step;
-            oka[u] = load(t, fa[u]);
-            okb[u] = load(t + 1, fb[u]);
-        }
-        for (int tile = t0; tile < tile_end; tile += NB * step) {
-#pragma unroll
-            for (int u = 0; u < NB; ++u) {
+            for (int u = 0; u < ST; ++u) {
                 const int t = tile + u * step;
                 if (t >= tile_end) break;
-                if (oka[u] > 0 || okb[u] > 0) process(fa[u], fb[u], oka[u], okb[u], t);
-                const int nt = t + NB * step;
-                oka[u] = load(nt, fa[u]);
-                okb[u] = load(nt + 1, fb[u]);
+                // the oldest pair in flight is this one
+                wait_loads<kLoadsPerPair * (ST - 1)>();
+                I4Frags<D> fa, fb;
+                fa.flags = flag_s[u][0];
+                fa.fword = fword_s[u][0];
+                fb.flags = flag_s[u][1];
+                fb.fword = fword_s[u][1];
+                const int capa = cap_s[u][0], capb = cap_s[u][1];
+                const int nva = max(0, min(capa, ctx - t * kTile));
+                const int nvb = max(0, min(capb, ctx - (t + 1) * kTile));
+                const bool live = capa > 0 || capb > 0;
+                float pr[8];
+                if (live) {
+                    fetch_k(stg[u][wave], 0, fa);
+                    fetch_k(stg[u][wave], 1, fb);
+                    scores(fa, fb, nva, nvb, t, pr);
+                    fetch_v(stg[u][wave], 0, fa);
+                    fetch_v(stg[u][wave], 1, fb);
+                }
+                // the stage is read: reload it with the pair ST steps ahead
+                wait_lds_reads();
+                issue(t + ST * step, u, next);
+                next = lookup(t + (ST + 1) * step);
+                if (live) pv(fa, fb, nva, nvb, pr);
             }
         }
+        // every load has landed before the ring is reused (the wave results below share
+        // its memory) or the wave ends
+        wait_loads<0>();
+        __syncthreads();
 
         // ---- wave result: column n < GW holds head n; lane (g, n) has d = 16j + 4g + r ----
         l_run = add_rows(l_run);
@@ -485,33 +614,35 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 for (int r = 0; r < 4; ++r) comb[wave][n][2 + 16 * j + 4 * g + r] = acc[j][r];
             }
             if (g == 0) {
-                comb[wave][n][0] = m_run;
+                // a wave that scored no token: exp2 of its state's max is 0 in the merge
+                comb[wave][n][0] = first ? -1e30f : m_run;
                 comb[wave][n][1] = l_run;
             }
         }
         __syncthreads();
         finish_segment<D, GW>(p, comb, b, hq0, U, tile_begin, tile_end, pos == ws.lo ? 0 : 1);
+        __syncthreads();  // the wave states are read before the next item's loads refill the ring
         pos = item0 + tile_end;
     }
 }
 
-#ifndef VSPEC_I4_PAIRS_IN_FLIGHT
-#define VSPEC_I4_PAIRS_IN_FLIGHT 1
+#ifndef VSPEC_I4_STAGES
+#define VSPEC_I4_STAGES 2
 #endif
 
 template <int D, int GW, bool USED>
 void launch_used(const DecodeParams& p, dim3 grid, hipStream_t s) {
-    constexpr int NB = VSPEC_I4_PAIRS_IN_FLIGHT;
+    constexpr int ST = VSPEC_I4_STAGES;
     if (p.read_flags) {
         if (p.block_tokens == 16)
-            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB, true, USED>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, ST, true, USED>), grid, dim3(256), 0, s, p);
         else
-            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, true, USED>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, ST, true, USED>), grid, dim3(256), 0, s, p);
     } else {
         if (p.block_tokens == 16)
-            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, NB, false, USED>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 16, ST, false, USED>), grid, dim3(256), 0, s, p);
         else
-            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, NB, false, USED>), grid, dim3(256), 0, s, p);
+            hipLaunchKernelGGL((decode_mfma_i4<D, GW, 0, ST, false, USED>), grid, dim3(256), 0, s, p);
     }
 }
 
