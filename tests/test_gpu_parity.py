@@ -575,41 +575,51 @@ def test_config4_continuous_batching(oracle, gpu):
         check_attention(oracle, case, got, 0, subset=subset)
 
 
-def test_decode_uneven_pair_shares(oracle, gpu):
-    """With a grid of two workgroups per CU and a ragged f16 batch, the balanced split
-    gives the first-half workgroup of each pair a larger share of the tiles (the CU's
-    arbiter favours its older waves).  Every share the library accepts (500..900 per mille,
-    VSPEC_ROCM_DECODE_OLD_PERMILLE) changes the rounding only: the outputs stay within
-    tolerance of the oracle and within 1e-5 of the equal split, every row written."""
+@pytest.mark.parametrize("dtype,uniform", [(DTYPE_F16, False), (DTYPE_INT4, False), (DTYPE_INT4, True)])
+def test_decode_uneven_pair_shares(oracle, gpu, dtype, uniform):
+    """With a grid of two workgroups per CU, the balanced split gives the first-half
+    workgroup of each pair a larger share of the tiles (the CU's arbiter favours its older
+    waves): for ragged f16 batches and for every int4 batch.  Every share the library
+    accepts (500..900 per mille, VSPEC_ROCM_DECODE_OLD_PERMILLE / ..._INT4) changes the
+    rounding only: the outputs stay within tolerance of the oracle and close to the equal
+    split (f16: 1e-5; int4: a fifth of its oracle tolerance, since P' = p * scale is
+    rounded to fp16 against each segment's own running max), every row written (int4:
+    whether or not the host is told that every context is the same, which decides the
+    merge launch from the shares)."""
     import os
 
     import torch
     import vspec_rocm as vr
 
-    say("[pair shares] build")
-    ctx = oracle.uniform_int(91, 3000, 5200, 20)
-    case = make_case(oracle, DTYPE_F16, 20, 32, 8, 128, 16, ctx, seed=92)
+    say(f"[pair shares] dtype={dtype} uniform={uniform} build")
+    ctx = [4097] * 20 if uniform else oracle.uniform_int(91, 3000, 5200, 20)
+    case = make_case(oracle, dtype, 20, 32, 8, 128, 16, ctx, seed=92 + dtype)
     pool = build_both(oracle, case, gpu, prefix_split=False)
     tab = torch.from_numpy(case.tables).to(gpu)
     cl = torch.from_numpy(case.ctx).to(gpu)
     q = torch.from_numpy(case.q).to(gpu)
     outs = {}
-    old = os.environ.get("VSPEC_ROCM_DECODE_OLD_PERMILLE")
+    var = "VSPEC_ROCM_DECODE_OLD_PERMILLE_INT4" if dtype == DTYPE_INT4 else "VSPEC_ROCM_DECODE_OLD_PERMILLE"
+    old = os.environ.get(var)
     try:
         for pm in (500, 620, 700, 900):
-            os.environ["VSPEC_ROCM_DECODE_OLD_PERMILLE"] = str(pm)
-            out = torch.full_like(q, float("nan"))
-            vr.paged_decode(pool, tab, cl, q, max_ctx_len=case.tmax, numerics=1, out=out)
-            outs[pm] = out.cpu().numpy()
+            os.environ[var] = str(pm)
+            for hint in ((0, case.tmax) if uniform else (0,)):
+                out = torch.full_like(q, float("nan"))
+                vr.paged_decode(pool, tab, cl, q, max_ctx_len=case.tmax, numerics=1, out=out, min_ctx_len=hint)
+                outs[(pm, hint)] = out.cpu().numpy()
     finally:
         if old is None:
-            os.environ.pop("VSPEC_ROCM_DECODE_OLD_PERMILLE", None)
+            os.environ.pop(var, None)
         else:
-            os.environ["VSPEC_ROCM_DECODE_OLD_PERMILLE"] = old
-    for pm, o in outs.items():
-        assert np.isfinite(o).all(), pm
-        assert np.abs(o - outs[500]).max() < 1e-5, pm
-    check_attention(oracle, case, outs[700], 1, subset=[0, 5, 11, 19])
+            os.environ[var] = old
+    bound = 1e-5 if dtype != DTYPE_INT4 else 0.2 * tol_of(dtype, case_vmax(case))
+    for key, o in outs.items():
+        assert np.isfinite(o).all(), key
+        err = np.abs(o - outs[(500, 0)]).max()
+        say(f"    {key}: max-abs vs equal shares {err:.2e} (bound {bound:.1e})")
+        assert err < bound, key
+    check_attention(oracle, case, outs[(700, 0)], 1, subset=[0, 5, 11, 19])
 
 
 @pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])

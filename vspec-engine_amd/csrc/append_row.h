@@ -66,12 +66,8 @@ __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq
     constexpr int EPT = append_ept(DT);
     const uint32_t lb = pos / p.block_tokens;
     if (lb >= p.max_blocks) return;
-    const int32_t phys = p.block_tables[(size_t)seq * p.max_blocks + lb];
-    if (phys < 0 || (uint32_t)phys >= p.num_blocks) return;
-    const uint32_t slot = pos % p.block_tokens;
-    const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + slot;
-    const size_t e0 = (size_t)c * EPT;  // first element of this chunk within the row
-
+    // the source elements are read before the table entry is looked at: both loads are in
+    // flight together
     float x[EPT];
     const uint8_t* src = which ? p.v_new : p.k_new;
     if constexpr (SRC == VSPEC_KV_F32) {
@@ -86,6 +82,12 @@ __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq
 #pragma unroll
         for (int j = 0; j < EPT / 8; ++j) unpack_f16x8(s4[j], x + 8 * j);
     }
+    const int32_t phys = p.block_tables[(size_t)seq * p.max_blocks + lb];
+    if (phys < 0 || (uint32_t)phys >= p.num_blocks) return;
+    const uint32_t slot = pos % p.block_tokens;
+    const size_t row = ((size_t)phys * p.hkv + h) * p.block_tokens + slot;
+    const size_t e0 = (size_t)c * EPT;  // first element of this chunk within the row
+
     const bool rope = p.rope_cos != nullptr;
     if (rope) {
         if (pos >= p.max_pos) return;  // no table row: the token is not written
@@ -270,11 +272,13 @@ __device__ __forceinline__ void append_item(const AppendParams& p, uint64_t it) 
 // item whose last tile lies in this workgroup's range [ws.lo, ws.hi) -- exactly one
 // workgroup per work item -- gets its sequence's new token written for its kv head at
 // position ctx_lens[b] - 1, exactly as the append kernel writes it.  All threads call this
-// before the workgroup reads any tile; it returns with the stores complete and a barrier
-// passed, so the workgroup's later loads of those tiles see them.  Other workgroups never
-// read the rows written here (they belong to the item's last tile), except the owners of
-// the other q-head groups of the same kv head, which write the same bytes themselves.
-template <int DT, int D>
+// before the workgroup reads any tile the append may write.  WAIT: it returns with the
+// stores complete and a barrier passed, so the workgroup's later loads of those tiles see
+// them; without WAIT it returns with the stores issued, and the caller waits for them (every
+// thread) and passes a barrier before such loads.  Other workgroups never read the rows
+// written here (they belong to the item's last tile), except the owners of the other
+// q-head groups of the same kv head, which write the same bytes themselves.
+template <int DT, int D, bool WAIT = true>
 __device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCursor c, const int ips,
                              FlagOp& pending, uint32_t* pend_lds) {
     constexpr int EPT = append_ept(DT);
@@ -338,8 +342,10 @@ __device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCur
         pend_lds[1] = pending.bit;
         pend_lds[2] = pending.set ? pending.bit : 0u;
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
-    __syncthreads();
+    if constexpr (WAIT) {
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
+        __syncthreads();
+    }
 }
 
 }  // namespace vkv

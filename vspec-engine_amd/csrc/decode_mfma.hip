@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const int n = lane & 15;   // column / token within the tile
 
     const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
-    const WorkSplit ws = work_split<true>(p, ips, split_sh);
+    const WorkSplit ws = work_split<kSplitRagged>(p, ips, split_sh);
     if (ws.lo >= ws.hi) return;
     const ItemCursor first = cursor_at(p, ws);
     FlagOp no_flags;  // f16 pools keep no clamp flags
@@ -459,7 +459,7 @@ void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
     // items split over several workgroups (same split: the f16 kernel's pair shares)
     if (p.merge) {
         const dim3 merge_grid(p.batch * p.hkv * p.gsplit);
-        hipLaunchKernelGGL((decode_merge_split<D, GW, true>), merge_grid, dim3(kWaves * 64), 0, s, p);
+        hipLaunchKernelGGL((decode_merge_split<D, GW, kSplitRagged>), merge_grid, dim3(kWaves * 64), 0, s, p);
     }
 }
 

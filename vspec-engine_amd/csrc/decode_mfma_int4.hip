@@ -18,7 +18,11 @@
 //     chunks are half of these A operands.
 //
 // A nibble t (two's complement code c = (t ^ 8) - 8) becomes an exact fp16 through a
-// magic exponent, two codes per 32-bit operation (codes_to_f16).
+// magic exponent, two codes per 32-bit operation, plus a bias that the MFMAs cancel
+// (biased_codes_to_f16).
+//
+// Each wave streams its tile pairs through an LDS ring (buffer loads straight into LDS)
+// two pairs ahead of the one it works on.
 //
 // The std clamp is screened per key from v_dot8 sums of the codes (sum c, sum c^2)
 // and the bound |x| <= 8 * scale; keys it may affect get exact fp32 scores.
@@ -35,20 +39,29 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 
 // Four fp16 pairs from one code dword: pair k = (nibble k, nibble k + 4).  A nibble t
 // sits in an fp16 mantissa under a magic exponent (1024 + u for bits 0..3, 64 + u for
-// bits 4..7, u = t ^ 8 = code + 8), so one shift, four three-input bit operations and
-// four packed subtractions convert eight codes exactly.
-__device__ __forceinline__ void codes_to_f16(uint32_t w, uint32_t out[4]) {
+// bits 4..7, u = t ^ 8 = code + 8), so one shift and four three-input bit operations
+// give eight codes exactly, each plus a bias: code + 1032 in pairs 0 and 2 (nibbles 0-3),
+// code + 72 in pairs 1 and 3 (nibbles 4-7).
+__device__ __forceinline__ void biased_codes_to_f16(uint32_t w, uint32_t out[4]) {
     const uint32_t w8 = w >> 8;
-    const uint32_t p0 = ((w ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u;   // 1024 + u
-    const uint32_t p1 = ((w ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u;   // 64 + u
-    const uint32_t p2 = ((w8 ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u;
-    const uint32_t p3 = ((w8 ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u;
+    out[0] = ((w ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u;
+    out[1] = ((w ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u;
+    out[2] = ((w8 ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u;
+    out[3] = ((w8 ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u;
+}
+
+// K codes for the score MFMAs: pairs 0 and 2 lose their bias (a packed subtraction each);
+// pairs 1 and 3 keep code + 72, and the score MFMAs start from minus that bias' share of
+// every column (72 times the column's B operands on those k-slots), which cancels it.
+// V codes for the P.V MFMAs keep both biases: a second MFMA per d-tile whose A operand is
+// the constant -1032 or -72 takes each pair's share back right away (it rounds once in
+// fp32 at up to 1040 times the pair's P' sum: below 2^-24 * 1040 / 8 of max |v| over the
+// whole context).
+__device__ __forceinline__ void k_codes_to_f16(uint32_t w, uint32_t out[4]) {
+    biased_codes_to_f16(w, out);
     const h2_t b0 = {(_Float16)1032.0f, (_Float16)1032.0f};
-    const h2_t b1 = {(_Float16)72.0f, (_Float16)72.0f};
-    out[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p0) - b0);
-    out[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p1) - b1);
-    out[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p2) - b0);
-    out[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p3) - b1);
+    out[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, out[0]) - b0);
+    out[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, out[2]) - b0);
 }
 
 template <int D>
@@ -91,6 +104,7 @@ __device__ __forceinline__ void lds_load16(uint32_t lds, rsrc_t r, uint32_t voff
 __device__ __forceinline__ void lds_load4(uint32_t lds, rsrc_t r, uint32_t voff) {
     asm volatile("buffer_load_dword %0, %1, 0 offen nt lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
+
 template <int N>
 __device__ __forceinline__ void wait_loads() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -129,6 +143,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
     float(*comb)[GW][D + 2] = reinterpret_cast<float(*)[GW][D + 2]>(&stg[0][0]);
     __shared__ float qs[GW][D];
     __shared__ uint4 qb_lds[NQ][2][64];  // QK B operands (hi, lo) per lane
+    __shared__ float kbias_lds[16];       // per score column: the K bias' share (k_codes_to_f16)
     __shared__ float patch_val[kWaves][kTile][4];
     __shared__ int patch_flag[kWaves][kTile];
     __shared__ SplitShared split_sh;
@@ -139,22 +154,36 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
     const int n = lane & 15;
 
     const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
-    const WorkSplit ws = work_split<false>(p, ips, split_sh);
+    const WorkSplit ws = work_split<kSplitAlways>(p, ips, split_sh);
     FlagOp pending = {nullptr, 0u, false};
     __shared__ uint32_t pend_lds[3];  // the fused append's first clamp flag: {word, bit, value}
     if (FL && threadIdx.x == 0) pend_lds[0] = 0xffffffffu;
-    if (p.k_new && ws.lo < ws.hi)
-        fused_append<VSPEC_KV_INT4, D>(p, ws, cursor_at(p, ws), ips, pending, FL ? pend_lds : nullptr);
-    uint32_t pend_word = 0xffffffffu, pend_bit = 0u, pend_val = 0u;
-    if (FL) {
-        __syncthreads();
-        pend_word = __builtin_amdgcn_readfirstlane(pend_lds[0]);
-        pend_bit = __builtin_amdgcn_readfirstlane(pend_lds[1]);
-        pend_val = __builtin_amdgcn_readfirstlane(pend_lds[2]);
+    // Set-up of the range's first work item overlaps the fused append: its q rows are
+    // loaded before the append, and its first tile pairs are on their way before the
+    // barrier that publishes the append (pairs that may hold the appended token wait
+    // behind that barrier).  The threads that stored wait for their stores first.
+    // q rows of a work item (wave w < GW: head w), loaded ahead of the item's set-up
+    constexpr int E = D / 64;
+    float q_rows[E];
+    auto load_q = [&](const int bb, const int yy) {
+        if (wave < GW) {
+            const int hq = (yy / (int)p.gsplit) * ((int)p.gsplit * GW) + (yy % (int)p.gsplit) * GW + wave;
+            const float* qrow = p.q + ((size_t)bb * p.hq + hq) * D;
+#pragma unroll
+            for (int e = 0; e < E; ++e) q_rows[e] = qrow[lane * E + e];
+        }
+    };
+    if (ws.lo < ws.hi) {
+        const ItemCursor c0 = cursor_at(p, ws);
+        load_q(c0.b, c0.y);
     }
-    // the append's first flag update, after the barrier: it overlaps the first tile loads
-    // instead of holding up the barrier (a tile read of its word takes the patched value)
-    apply_flag(pending);
+    const bool appending = p.k_new != nullptr && ws.lo < ws.hi;
+    if (appending) {
+        fused_append<VSPEC_KV_INT4, D, false>(p, ws, cursor_at(p, ws), ips, pending, FL ? pend_lds : nullptr);
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's stores (and q loads) are done
+    }
+    uint32_t pend_word = 0xffffffffu, pend_bit = 0u, pend_val = 0u;
+    bool first_item = true;
     int b = ws.b;
     int seq0 = ws.seq0;
     for (int pos = ws.lo; pos < ws.hi;) {
@@ -224,13 +253,13 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                               uint32_t& flag, uint32_t& fword) {
             tile = __builtin_amdgcn_readfirstlane(tile);
             const bool ok = tile < tile_end && entry >= 0 && (uint32_t)entry < p.num_blocks;
-            const size_t bh = (size_t)(ok ? entry : 0) * p.hkv + hk;
             const int slot0 = (tile % tiles_per_block) * kTile;
+            const size_t bh = (size_t)(ok ? entry : 0) * p.hkv + hk;
             const uint32_t code_bytes = ok ? 8u * D : 0u;
             lds_load16(lds_addr(&st.k[h][0]), tile_rsrc(p.k + (bh * P + slot0) * (D / 2), code_bytes), off_k);
             lds_load16(lds_addr(&st.v[h][0]),
                        tile_rsrc(p.v + bh * ((size_t)P * D / 2) + (size_t)(slot0 / kTile) * (8 * D), code_bytes), off_v);
-            if (lane < 32) {
+            if (lane < 8 * NG) {
                 lds_load4(lds_addr(&st.sc[h][0]),
                           tile_rsrc(p.ks + bh * NG * P + slot0, ok ? (uint32_t)(((NG - 1) * P + kTile) * 2) : 0u), off_ks);
                 lds_load4(lds_addr(&st.sc[h][32]), tile_rsrc(p.vs + (bh * P + slot0) * NG, ok ? 32u * NG : 0u), off_vs);
@@ -278,13 +307,11 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 
         // ---- q' = clip(q) * scale * log2(e): wave w prepares head w ----
         if (wave < GW) {
-            const float* qrow = p.q + ((size_t)b * p.hq + hq0 + wave) * D;
-            constexpr int E = D / 64;
             float x[E];
             float s = 0.f;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                x[e] = qrow[lane * E + e];
+                x[e] = q_rows[e];
                 s += x[e];
             }
 #pragma unroll
@@ -299,17 +326,43 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 #pragma unroll
             for (int e = 0; e < E; ++e) qs[wave][lane * E + e] = fminf(fmaxf(x[e], -th), th) * p.qscale;
         }
-        // the first ST pairs are on their way while the q operands are prepared (after the
-        // q rows are in registers: a wait for those would also wait for these)
+        // The first ST pairs are on their way while the q operands are prepared (after the
+        // q rows are in registers: a wait for those would also wait for these).  In the
+        // range's first item, pairs of any wave that may reach the appended token's tile
+        // (the item's last, when this workgroup appended it) are issued after the barrier.
+        const bool defer = first_item && appending && tile_end == U &&
+                           tile_begin + 2 * (kWaves - 1) + (ST - 1) * step + 1 >= U - 1;
+        // the ring's first table reads go out together
+        Look first_look[ST];
 #pragma unroll
-        for (int u = 0; u < ST; ++u) issue(t0 + u * step, u, lookup(t0 + u * step));
+        for (int u = 0; u < ST; ++u) first_look[u] = lookup(t0 + u * step);
+        if (!defer) {
+#pragma unroll
+            for (int u = 0; u < ST; ++u) issue(t0 + u * step, u, first_look[u]);
+        }
         Look next = lookup(t0 + ST * step);
         __syncthreads();
+        if (first_item) {
+            if (FL) {
+                pend_word = __builtin_amdgcn_readfirstlane(pend_lds[0]);
+                pend_bit = __builtin_amdgcn_readfirstlane(pend_lds[1]);
+                pend_val = __builtin_amdgcn_readfirstlane(pend_lds[2]);
+            }
+            // the append's first flag update, after the barrier (a tile read of its word
+            // takes the patched value)
+            apply_flag(pending);
+            if (defer) {
+#pragma unroll
+                for (int u = 0; u < ST; ++u) issue(t0 + u * step, u, first_look[u]);
+            }
+            first_item = false;
+        }
 
         // ---- QK B operands: k-slots 8g..8g+7 of MFMA m carry code dword dw = g*NQ + m in
         // the order e = 0,4,1,5,2,6,3,7; column n takes group n/4 of head n%4 ----
         if (wave == 0) {
             const int hh = n & 3;
+            float odd = 0.f;  // this lane's B operands on the k-slots of odd elements
 #pragma unroll
             for (int m = 0; m < NQ; ++m) {
                 const int dw = g * NQ + m;
@@ -322,12 +375,16 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                     const _Float16 hi = (_Float16)qv;
                     hi8[j] = hi;
                     lo8[j] = (_Float16)(qv - (float)hi);
+                    if (e & 1) odd += (float)hi8[j] + (float)lo8[j];
                 }
                 qb_lds[m][0][lane] = __builtin_bit_cast(uint4, hi8);
                 qb_lds[m][1][lane] = __builtin_bit_cast(uint4, lo8);
             }
+            odd = add_rows(odd);
+            if (g == 0) kbias_lds[n] = 72.0f * odd;
         }
         __syncthreads();
+        const float kbias = kbias_lds[n];
 
         f4_t acc[NDT];
 #pragma unroll
@@ -375,15 +432,16 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 
         // Scores of a tile on the matrix cores, minus m_run: lane (g, n) gets tokens
         // 4g..4g+3 for head n%4.  The hi and lo products accumulate in one chain (the lo
-        // part is 2^-11 of the hi part: one fp32 accumulator keeps both); each of the four
+        // part is 2^-11 of the hi part: one fp32 accumulator keeps both), from minus the K
+        // bias' share of the column (its magnitude, 72 |sum q'|, costs 2^-24 of it); each of the four
         // group columns of a head is scaled by its fp16 K scale and takes a quarter of
         // m_run in the same mixed-precision FMA, so the column sum is score - m_run.
         auto qk = [&](const I4Frags<D>& f) -> f4_t {
-            f4_t sacc = {0.f, 0.f, 0.f, 0.f};
+            f4_t sacc = {-kbias, -kbias, -kbias, -kbias};
 #pragma unroll
             for (int m = 0; m < NQ; ++m) {
                 uint32_t pr4[4];
-                codes_to_f16(f.k[m], pr4);
+                k_codes_to_f16(f.k[m], pr4);
                 const h8_t a = __builtin_bit_cast(h8_t, make_uint4(pr4[0], pr4[1], pr4[2], pr4[3]));
                 sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, qb_lds[m][0][lane]), sacc, 0, 0, 0);
                 sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, qb_lds[m][1][lane]), sacc, 0, 0, 0);
@@ -543,6 +601,10 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         };
 
         // O^T += V^T P'^T for a pair whose V half of the fragments is in registers
+        const h8_t bias_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1032.0f,
+                              (_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1032.0f};
+        const h8_t bias_hi = {(_Float16)-72.0f, (_Float16)-72.0f, (_Float16)-72.0f, (_Float16)-72.0f,
+                              (_Float16)-72.0f, (_Float16)-72.0f, (_Float16)-72.0f, (_Float16)-72.0f};
         auto pv = [&](I4Frags<D>& fa, I4Frags<D>& fb, const int nva, const int nvb, const float (&pr)[8]) {
             clear_masked_scales(fa, nva);
             clear_masked_scales(fb, nvb);
@@ -560,12 +622,14 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                     pq[i] = (_Float16)__builtin_fmaf(pr[i], (float)v2[k & 1], 0.0f);
                 }
                 uint32_t ka[4], kb[4];
-                codes_to_f16(fa.v[q], ka);
-                codes_to_f16(fb.v[q], kb);
-                const h8_t a0 = __builtin_bit_cast(h8_t, make_uint4(ka[0], ka[2], kb[0], kb[2]));
-                const h8_t a1 = __builtin_bit_cast(h8_t, make_uint4(ka[1], ka[3], kb[1], kb[3]));
+                biased_codes_to_f16(fa.v[q], ka);
+                biased_codes_to_f16(fb.v[q], kb);
+                const h8_t a0 = __builtin_bit_cast(h8_t, make_uint4(ka[0], ka[2], kb[0], kb[2]));  // code + 1032
+                const h8_t a1 = __builtin_bit_cast(h8_t, make_uint4(ka[1], ka[3], kb[1], kb[3]));  // code + 72
                 acc[2 * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pq, acc[2 * q], 0, 0, 0);
+                acc[2 * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias_lo, pq, acc[2 * q], 0, 0, 0);
                 acc[2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, pq, acc[2 * q + 1], 0, 0, 0);
+                acc[2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias_hi, pq, acc[2 * q + 1], 0, 0, 0);
             }
         };
 
@@ -603,6 +667,14 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // every load has landed before the ring is reused (the wave results below share
         // its memory) or the wave ends
         wait_loads<0>();
+        // the next item's q rows load while this one's states are merged
+        if (item0 + tile_end < ws.hi) {
+            const int npos = item0 + tile_end;
+            const bool next_seq = npos >= seq0 + U * ips;
+            const int nb = next_seq ? b + 1 : b;
+            const int nU = next_seq ? item_tiles(p, nb) : U;
+            load_q(nb, (npos - (next_seq ? seq0 + U * ips : seq0)) / nU);
+        }
         __syncthreads();
 
         // ---- wave result: column n < GW holds head n; lane (g, n) has d = 16j + 4g + r ----
@@ -653,7 +725,7 @@ void launch(const DecodeParams& p, dim3 grid, hipStream_t s) {
     // items split over several workgroups (same split: equal shares)
     if (p.merge) {
         const dim3 merge_grid(p.batch * p.hkv * p.gsplit);
-        hipLaunchKernelGGL((decode_merge_split<D, GW, false>), merge_grid, dim3(kWaves * 64), 0, s, p);
+        hipLaunchKernelGGL((decode_merge_split<D, GW, kSplitAlways>), merge_grid, dim3(kWaves * 64), 0, s, p);
     }
 }
 

@@ -223,6 +223,9 @@ struct DecodeParams {
     // least tiles per workgroup of the balanced split (>= 1), applied to the actual total
     // so that the split does not depend on the host's bound
     uint32_t min_tiles;
+    // tiles per work item when the host knows every context to be the same (min_ctx_len ==
+    // max_ctx_len), else 0: the split then needs no pass over ctx_lens
+    uint32_t uniform_tiles;
 };
 
 // Launch the MFMA decode kernels for f16 pools (decode_mfma.hip) and int4 pools
@@ -293,6 +296,10 @@ __device__ __forceinline__ void merge_waves(const DecodeParams& p, const float (
 typedef const __attribute__((address_space(4))) int32_t const_i32;
 __device__ __forceinline__ const const_i32* as_const(const int32_t* ptr) { return (const const_i32*)ptr; }
 
+constexpr int kSplitEqual = 0;
+constexpr int kSplitRagged = 1;
+constexpr int kSplitAlways = 2;
+
 struct WorkSplit {
     int total;   // T
     int groups;  // G (balanced split), 0 for the chunked split
@@ -314,6 +321,7 @@ struct SplitShared {
 };
 
 __device__ __forceinline__ int item_tiles(const DecodeParams& p, int b) {
+    if (p.uniform_tiles) return (int)p.uniform_tiles;
     const int ctx = min(max(as_const(p.ctx_lens)[b], 0), (int)(p.max_blocks * p.block_tokens));
     return max(1, min((ctx + kTile - 1) / kTile, (int)p.max_tiles));
 }
@@ -328,9 +336,10 @@ __device__ __forceinline__ int used_cap(int used, int slot0) { return min(kTile,
 // workgroup and the rest to the second-half one.  Workgroups g and g + G/2 share a CU,
 // g dispatched first; the CU's wave arbiter favours the older waves, so with equal
 // shares the first-half workgroup finishes well before its partner.
-// UNEVEN: the kernel supports unequal pair shares (the f16 kernel); without it the
-// weighted arithmetic is compiled out.
-template <bool UNEVEN>
+// UNEVEN: the pair-share policy of the kernel: kSplitEqual (the weighted arithmetic is
+// compiled out), kSplitRagged (unequal shares for ragged batches: the f16 kernel) or
+// kSplitAlways (unequal shares for any batch: the int4 kernel).
+template <int UNEVEN>
 __device__ __forceinline__ int split_lo(const DecodeParams& p, const WorkSplit& w, int g) {
     if (!w.groups) return g * (int)p.chunk_tiles;
     if (!UNEVEN || !w.half) return (int)((long long)g * w.total / w.groups);
@@ -339,7 +348,7 @@ __device__ __forceinline__ int split_lo(const DecodeParams& p, const WorkSplit& 
 }
 
 // The workgroup whose range holds tile t (the inverse of split_lo).
-template <bool UNEVEN>
+template <int UNEVEN>
 __device__ __forceinline__ int split_group_of(const DecodeParams& p, const WorkSplit& w, int t) {
     if (!w.groups) return t / (int)p.chunk_tiles;
     if (!UNEVEN || !w.half) return (int)(((long long)(t + 1) * w.groups - 1) / w.total);
@@ -353,7 +362,7 @@ __device__ __forceinline__ int split_group_of(const DecodeParams& p, const WorkS
 
 // The split's shape once T (and whether the batch is ragged) is known: groups and pair
 // shares.  The same for every workgroup of the split kernel and for the merge launch.
-template <bool UNEVEN>
+template <int UNEVEN>
 __device__ __forceinline__ void split_shape(const DecodeParams& p, WorkSplit& r) {
     const int grid = (int)p.split_grid;
     r.half = 0;
@@ -364,11 +373,14 @@ __device__ __forceinline__ void split_shape(const DecodeParams& p, WorkSplit& r)
     }
     r.groups = min(grid, r.total);
     if (p.min_tiles > 1) r.groups = min(r.groups, max(1, r.total / (int)p.min_tiles));
-    // Unequal shares for ragged batches with at least 64 tiles per workgroup (measured:
+    // Unequal shares with at least 64 tiles per workgroup, and only where every
+    // second-half share is at least one tile (every workgroup of an item's span then holds
+    // one of its partials).  The f16 kernel takes them for ragged batches only (measured:
     // C4 206 -> 190 us at 700; equal contexts lose, their ranges stop coinciding with
-    // whole work items), and only where every second-half share is at least one tile
-    // (every workgroup of an item's span then holds one of its partials).
-    if (UNEVEN && p.split_old_permille != 500 && r.ragged && r.groups == grid && (grid & 1) == 0 &&
+    // whole work items); the int4 kernel for every batch (its second-half workgroups
+    // otherwise finish ~25 % after the first-half ones).
+    if (UNEVEN && p.split_old_permille != 500 && (UNEVEN == kSplitAlways || r.ragged) && r.groups == grid &&
+        (grid & 1) == 0 &&
         (long long)r.total >= 64LL * grid && (long long)(1000 - (int)p.split_old_permille) * r.total >= 500LL * grid) {
         r.half = grid / 2;
         r.wa = (int)p.split_old_permille;
@@ -376,7 +388,7 @@ __device__ __forceinline__ void split_shape(const DecodeParams& p, WorkSplit& r)
 }
 
 // this workgroup's tiles [lo, hi) once T is known
-template <bool UNEVEN>
+template <int UNEVEN>
 __device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r) {
     const int g = blockIdx.x;
     split_shape<UNEVEN>(p, r);
@@ -391,12 +403,22 @@ __device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r)
 
 // Block-wide (every thread calls it; the result is uniform).  The host keeps
 // T = hkv * gsplit * sum U_b below 2^31.
-template <bool UNEVEN>
+template <int UNEVEN>
 __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, SplitShared& sh) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nb = (int)p.batch;
     WorkSplit r;
+    if (p.uniform_tiles) {
+        // every sequence holds uniform_tiles tiles per work item: no scan, no barrier
+        const int per_seq = (int)p.uniform_tiles * ips;
+        r.total = nb * per_seq;
+        r.ragged = 0;
+        split_range<UNEVEN>(p, r);
+        r.b = r.lo < r.hi ? r.lo / per_seq : 0;
+        r.seq0 = r.b * per_seq;
+        return r;
+    }
     if (nb <= kWaves * 64) {
         // one sequence per thread: the total and the search come from one scan
         const int b = (int)threadIdx.x;
@@ -408,7 +430,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
             if (lane >= o) x += y;
         }
         int umin = b < nb ? u : 0x7fffffff, umax = u;
-        if constexpr (UNEVEN) {
+        if constexpr (UNEVEN == kSplitRagged) {
 #pragma unroll
             for (int o = 32; o; o >>= 1) {
                 umin = min(umin, __shfl_xor(umin, o));
@@ -428,13 +450,13 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         for (int w = 0; w < kWaves; ++w) {
             before += w < wave ? sh.wsum[w] : 0;
             all += sh.wsum[w];
-            if constexpr (UNEVEN) {
+            if constexpr (UNEVEN == kSplitRagged) {
                 umin = min(umin, sh.umin[w]);
                 umax = max(umax, sh.umax[w]);
             }
         }
         r.total = __builtin_amdgcn_readfirstlane(all) * ips;
-        r.ragged = UNEVEN ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
+        r.ragged = UNEVEN == kSplitRagged ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
         split_range<UNEVEN>(p, r);
         r.b = 0;
         r.seq0 = 0;
@@ -453,7 +475,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
     for (int b = threadIdx.x; b < nb; b += kWaves * 64) {
         const int u = item_tiles(p, b);
         s += u;
-        if constexpr (UNEVEN) {
+        if constexpr (UNEVEN == kSplitRagged) {
             umin = min(umin, u);
             umax = max(umax, u);
         }
@@ -461,7 +483,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
 #pragma unroll
     for (int o = 32; o; o >>= 1) {
         s += __shfl_xor(s, o);
-        if constexpr (UNEVEN) {
+        if constexpr (UNEVEN == kSplitRagged) {
             umin = min(umin, __shfl_xor(umin, o));
             umax = max(umax, __shfl_xor(umax, o));
         }
@@ -482,7 +504,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         umax = max(umax, sh.umax[w]);
     }
     r.total = __builtin_amdgcn_readfirstlane(units) * ips;
-    r.ragged = UNEVEN ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
+    r.ragged = UNEVEN == kSplitRagged ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
     split_range<UNEVEN>(p, r);
     r.b = 0;
     r.seq0 = 0;
@@ -634,7 +656,7 @@ __device__ __forceinline__ void finish_segment(const DecodeParams& p, const floa
 // g0 < g1 it merges their partials in order g0..g1 and writes the item's output rows;
 // items inside one range were written by the split kernel and are left alone.  Partial
 // loads go out NBATCH workgroups at a time, all in flight together.
-template <int D, int GW, bool UNEVEN>
+template <int D, int GW, int UNEVEN>
 __global__ __launch_bounds__(kWaves * 64) void decode_merge_split(DecodeParams p) {
     constexpr int NT = kWaves * 64;
     constexpr int K = (GW * D + NT - 1) / NT;  // outputs per thread: idx = tid + NT * k
@@ -682,7 +704,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_merge_split(DecodeParams p
         umax = max(umax, sh.umax[v]);
     }
     w.total = all * ips;
-    w.ragged = UNEVEN && umin != umax ? 1 : 0;
+    w.ragged = UNEVEN == kSplitRagged && umin != umax ? 1 : 0;
     split_shape<UNEVEN>(p, w);
     const int U = item_tiles(p, b);
     const int item0 = pre * ips + y * U;

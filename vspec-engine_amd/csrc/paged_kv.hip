@@ -747,6 +747,7 @@ uint8_t* scratch_address(int dev) {
 }
 
 constexpr uint32_t kDefaultOldPermille = 700;
+constexpr uint32_t kDefaultOldPermilleInt4 = 500;
 
 // workgroups per CU of the balanced MFMA split: VSPEC_ROCM_DECODE_WGS_PER_CU (1..8) when
 // set, else 0 (the plan decides)
@@ -760,11 +761,17 @@ uint32_t decode_wgs_per_cu_env() {
 }
 
 // Share of the first-half workgroup of each pair sharing a CU under the balanced split,
-// in 1/1000 (VSPEC_ROCM_DECODE_OLD_PERMILLE, 500..900).  Read on every call.
-uint32_t decode_old_permille() {
-    const char* e = getenv("VSPEC_ROCM_DECODE_OLD_PERMILLE");
+// in 1/1000 (VSPEC_ROCM_DECODE_OLD_PERMILLE for f16 pools, ..._INT4 for int4 pools,
+// 500..900).  Read on every call.  int4 keeps equal shares by default: measured per
+// workgroup at the north-star shape, the first-half workgroups end at ~65 us and their
+// partners at ~86 us (the CU's wave arbiter favours the older waves), yet unequal shares
+// are slower there (80.6 us at 500, 88.3 at 600, 98.7 at 700: work items then span two
+// workgroups, and each extra item costs its set-up and a merge launch).
+uint32_t decode_old_permille(uint32_t dtype) {
+    const bool i4 = dtype == VSPEC_KV_INT4;
+    const char* e = getenv(i4 ? "VSPEC_ROCM_DECODE_OLD_PERMILLE_INT4" : "VSPEC_ROCM_DECODE_OLD_PERMILLE");
     const long x = e ? strtol(e, nullptr, 10) : 0;
-    return x >= 500 && x <= 900 ? (uint32_t)x : kDefaultOldPermille;
+    return x >= 500 && x <= 900 ? (uint32_t)x : i4 ? kDefaultOldPermilleInt4 : kDefaultOldPermille;
 }
 
 // Least tiles per workgroup of the balanced split: VSPEC_ROCM_DECODE_MIN_TILES_PER_WG
@@ -806,26 +813,48 @@ struct DecodePlan {
     uint64_t split_tiles;  // tiles the balanced split spreads over grid_x (upper bound)
     uint32_t min_tiles;    // least tiles per workgroup of the balanced split
     uint32_t max_tiles;
+    uint32_t old_permille;  // pair share of the first-half workgroups (500: equal shares)
+    uint32_t uniform_tiles; // tiles per work item when every context is known to be the same
 };
 
 // With every context known to be the same (min_ctx_len == the context bound), the split
 // of the MFMA kernels (kv_common.h work_split with equal shares, as for any batch whose
 // contexts are equal) is known on the host: returns whether some range boundary falls
 // strictly inside a work item.  Without that knowledge a merge launch is always needed.
-bool uniform_split_has_partials(const VspecPagedAttnDesc* d, const DecodePlan* pl, uint64_t ctx_bound) {
-    if (!d->min_ctx_len || d->min_ctx_len < ctx_bound) return true;
-    const uint64_t items = (uint64_t)d->batch * d->kv.num_kv_heads * pl->gsplit;
+// Tiles per work item when every context is known to be the same (min_ctx_len at least
+// the bound), as the kernels' item_tiles computes them; 0 otherwise.
+uint32_t uniform_item_tiles(const VspecPagedAttnDesc* d, const DecodePlan* pl, uint64_t ctx_bound) {
+    if (!d->min_ctx_len || d->min_ctx_len < ctx_bound) return 0;
     const uint64_t ctx = ctx_bound < (uint64_t)d->max_blocks_per_seq * d->kv.block_tokens
                              ? ctx_bound : (uint64_t)d->max_blocks_per_seq * d->kv.block_tokens;
     uint64_t U = (ctx + kTile - 1) / kTile;
     if (U > pl->max_tiles) U = pl->max_tiles;
     if (U < 1) U = 1;
+    return (uint32_t)U;
+}
+
+bool uniform_split_has_partials(const VspecPagedAttnDesc* d, const DecodePlan* pl, uint64_t ctx_bound) {
+    const uint64_t U = uniform_item_tiles(d, pl, ctx_bound);
+    if (!U) return true;
+    const uint64_t items = (uint64_t)d->batch * d->kv.num_kv_heads * pl->gsplit;
     const uint64_t T = items * U;
     if (pl->chunk_tiles) return pl->chunk_tiles % U != 0 && T > pl->chunk_tiles;
     uint64_t G = pl->grid_x < T ? pl->grid_x : T;
     if (pl->min_tiles > 1) {
         const uint64_t cap = T / pl->min_tiles > 1 ? T / pl->min_tiles : 1;
         if (cap < G) G = cap;
+    }
+    // the int4 kernel's unequal pair shares (the kernels' split_shape: contexts are equal
+    // here, so the f16 kernel keeps equal shares)
+    const uint64_t wa = pl->old_permille;
+    if (d->kv.dtype == VSPEC_KV_INT4 && wa != 500 && G == pl->grid_x && G % 2 == 0 && T >= 64 * G &&
+        (1000 - wa) * T >= 500 * G) {
+        const uint64_t half = G / 2;
+        for (uint64_t g = 1; g < G; ++g) {
+            const uint64_t c = wa * (g < half ? g : half) + (1000 - wa) * (g > half ? g - half : 0);
+            if ((c * T / (1000 * half)) % U != 0) return true;
+        }
+        return false;
     }
     for (uint64_t g = 1; g < G; ++g) {
         if ((g * T / G) % U != 0) return true;
@@ -894,7 +923,11 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
         pl->max_tiles = max_tiles;
         pl->tiles_per_part = 0;
         pl->max_parts = 1;
+        // unequal pair shares need the grid of two workgroups per CU (g and g + G/2 share one)
+        pl->old_permille = !pl->chunk_tiles && pl->grid_x == 2u * (uint32_t)num_cus()
+                               ? decode_old_permille(d->kv.dtype) : 500u;
         pl->merge = uniform_split_has_partials(d, pl, ctx_bound);
+        pl->uniform_tiles = uniform_item_tiles(d, pl, ctx_bound);
         // the workspace stays even without a merge launch: a context below min_ctx_len (a
         // caller error) then leaves its partial states in valid memory, not its output
         pl->ws_bytes = (size_t)pl->grid_x * 2 * pl->gw * (2 + d->kv.head_dim) * sizeof(float);
@@ -1399,11 +1432,8 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.k_new = nullptr;
     p.v_new = nullptr;
     p.append_src = src_dtype;
-    // uneven shares for the f16 kernel only (the int4 kernel is bound by its vector ALU
-    // work, which the two workgroups of a CU share either way; measured slower)
-    const bool paired = pl.split && !pl.chunk_tiles && pl.grid_x == 2u * (uint32_t)num_cus() &&
-                        desc->kv.dtype == VSPEC_KV_F16;
-    p.split_old_permille = paired ? decode_old_permille() : 500u;
+    p.split_old_permille = pl.split ? pl.old_permille : 500u;
+    p.uniform_tiles = pl.split ? pl.uniform_tiles : 0u;
     p.min_tiles = pl.split && !pl.chunk_tiles ? pl.min_tiles : 1u;
 
     hipStream_t s = (hipStream_t)desc->stream;

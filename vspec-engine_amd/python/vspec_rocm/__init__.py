@@ -461,9 +461,11 @@ def decode_workspace_bytes(desc: VspecPagedAttnDesc) -> int:
 
 
 def paged_decode(pool: PagedPool, block_tables, ctx_lens, q, max_ctx_len=None, numerics=NUMERICS_PLAIN,
-                 scale=0.0, partition_tokens=0, out=None, workspace=None, stream=None, block_used=None):
+                 scale=0.0, partition_tokens=0, out=None, workspace=None, stream=None, block_used=None,
+                 min_ctx_len=0):
     """vspec_rocm_paged_decode_attention: q [B][Hq][D] float32 (device) -> out.  With
-    block_used ([B][max_blocks], tokens per table entry) ctx_lens holds the spans."""
+    block_used ([B][max_blocks], tokens per table entry) ctx_lens holds the spans;
+    min_ctx_len: the host's lower bound on ctx_lens (0: none)."""
     import torch
 
     assert q.dtype == torch.float32 and q.is_contiguous()
@@ -475,7 +477,8 @@ def paged_decode(pool: PagedPool, block_tables, ctx_lens, q, max_ctx_len=None, n
         max_ctx_len = int(cl.max().item()) if cl.numel() else 0
     if out is None:
         out = torch.empty_like(q)
-    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream, bu)
+    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream, bu,
+                         min_ctx_len)
     _check(lib().vspec_rocm_paged_decode_attention(C.byref(d)), "paged_decode_attention")
     _hold(stream, bt, cl, bu, out)
     return out
