@@ -67,6 +67,13 @@ def algorithmic_bytes(ctx_lens, Hq, Hkv, D, P, dtype):
     return kv + tables + qo
 
 
+def tiles_per_launch(ctx_lens, Hq, Hkv):
+    """16-token tiles the decode kernels stream per launch: one per 16 tokens of every
+    (sequence, kv head, group of up to 4 query heads) work item."""
+    groups = max(1, (Hq // Hkv) // 4)
+    return sum(max(1, (int(t) + 15) // 16) for t in ctx_lens) * Hkv * groups
+
+
 def cpu_baseline(args, wl, pool, tables, ctx, q_all, out_gpu, mode):
     """Time the reference CPU decode step on the first `cpu_seqs` sequences."""
     import numpy as np
@@ -372,7 +379,8 @@ def run_c5(args, wl, kv_dtype, mode):
         "roofline": {"bound": "hbm", "achieved": gbs(decode_bytes, stage[2]), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": gbs(decode_bytes, stage[2]) / PEAK_GBS, "traffic": load_traffic(args.workload),
                      "kernel": "decode_mfma_i4",
-                     "algorithmic_bytes_per_launch": decode_bytes},
+                     "algorithmic_bytes_per_launch": decode_bytes,
+                     "tiles_per_launch": tiles_per_launch(ctxs, Hq, Hkv)},
     }
 
 
@@ -627,7 +635,8 @@ def main():
                      "kernel": ("kv_append + " if args.separate_append else "") +
                                {"f16": "decode_mfma_f16", "int4": "decode_mfma_i4",
                                 "f32": "decode_partial" + (" + decode_combine" if ws_bytes else "")}[wl["dtype"]],
-                     "algorithmic_bytes_per_launch": alg},
+                     "algorithmic_bytes_per_launch": alg,
+                     "tiles_per_launch": tiles_per_launch(lens, Hq, Hkv)},
     }
     if not args.no_probe:
         log("probe ceilings ...")
