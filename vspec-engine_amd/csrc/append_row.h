@@ -271,8 +271,10 @@ __device__ __forceinline__ void append_item(const AppendParams& p, uint64_t it) 
 // Fused decode-step append of the MFMA decode kernels (p.k_new != null).  Every work
 // item whose last tile lies in this workgroup's range [ws.lo, ws.hi) -- exactly one
 // workgroup per work item -- gets its sequence's new token written for its kv head at
-// position ctx_lens[b] - 1, exactly as the append kernel writes it.  All threads call this
-// before the workgroup reads any tile the append may write.  WAIT: it returns with the
+// position ctx_lens[b] - 1, exactly as the append kernel writes it.  Threads below kItems
+// (the first lanes of wave 0) write the rows: with WAIT every thread calls this (it ends in a
+// barrier), without WAIT at least those, before the workgroup reads any tile the append may
+// write.  WAIT: it returns with the
 // stores complete and a barrier passed, so the workgroup's later loads of those tiles see
 // them; without WAIT it returns with the stores issued, and the caller waits for them (every
 // thread) and passes a barrier before such loads.  Other workgroups never read the rows

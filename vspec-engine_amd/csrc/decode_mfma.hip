@@ -74,8 +74,6 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const WorkSplit ws = work_split<kSplitRagged>(p, ips, split_sh);
     if (ws.lo >= ws.hi) return;
     const ItemCursor first = cursor_at(p, ws);
-    FlagOp no_flags;  // f16 pools keep no clamp flags
-    if (p.k_new) fused_append<VSPEC_KV_F16, D>(p, ws, first, ips, no_flags, nullptr);
 
 
     // ---- q' = clip(q) * scale * log2(e) of work item c (segment s) for this wave, and
@@ -388,26 +386,82 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const int nt = wave < len ? (len - wave + kWaves - 1) / kWaves : 0;
     Frags<D> f[NB];
     int ok[NB];
-    // the first tiles' loads go out before the q rows are staged, so that the two
-    // latencies overlap (the barrier below does not wait for them)
-#pragma unroll
-    for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * kWaves, f[u]);
-    // q rows of the first kQStage segments (rows GW*y .. GW*y + GW - 1 of sequence b are
-    // contiguous); merge slot s serves segment s first
-    {
+    // Set-up.  Wave 0 loads the q rows of the range's first kQStage segments (rows GW*y ..
+    // GW*y + GW - 1 of sequence b are contiguous; merge slot s serves segment s first) and
+    // writes the fused append's token rows, waits for both (nothing else of it is in
+    // flight, so the wait is short), stages the q rows in LDS, then issues its first NB
+    // tiles.  Waves 1.. issue their first NB tiles at once.  The barrier (an LDS-only wait:
+    // the other waves' tile loads stay in flight) publishes the q rows and the appended
+    // rows, and every wave prepares its q operands while its tiles are on the way.  A wave
+    // whose first NB tiles include a tile this workgroup appends into (the last tile of
+    // an item ending in the range) issues them after the barrier.
+    constexpr int QPL = (GW * D + 63) / 64;  // q floats per lane of wave 0 and segment
+    bool defer = false;
+    if (p.k_new && wave != 0) {
         ItemCursor c = first;
-        for (int s = 0; s < kQStage; ++s) {
-            const float* qrow = p.q + ((size_t)c.b * p.hq + (size_t)c.y * GW) * D;
-            for (int i = threadIdx.x; i < GW * D; i += kWaves * 64) qraw[s][i / D][i % D] = qrow[i];
-            if (c.item0 + c.U >= ws.hi) break;
+        const int end = min(ws.hi, ws.lo + NB * kWaves);
+        while (true) {
+            const int last = c.item0 + c.U - 1;
+            if (last >= ws.lo && last < end && (last - ws.lo) % kWaves == wave) defer = true;
+            if (c.item0 + c.U >= end) break;
             cursor_next(p, ips, c);
         }
-        if (threadIdx.x < kSlots) {
-            slot_cnt[threadIdx.x] = 0;
-            slot_seg[threadIdx.x] = threadIdx.x;
+    }
+    if (wave == 0) {
+        int nseg = 1;
+        {
+            ItemCursor c = first;
+            while (nseg < kQStage && c.item0 + c.U < ws.hi) {
+                cursor_next(p, ips, c);
+                ++nseg;
+            }
+        }
+        float qreg[kQStage][QPL];
+        {
+            ItemCursor c = first;
+#pragma unroll
+            for (int s = 0; s < kQStage; ++s) {
+                if (s < nseg) {
+                    const float* qrow = p.q + ((size_t)c.b * p.hq + (size_t)c.y * GW) * D;
+#pragma unroll
+                    for (int j = 0; j < QPL; ++j) {
+                        const int i = lane + 64 * j;
+                        qreg[s][j] = i < GW * D ? qrow[i] : 0.f;
+                    }
+                    if (s + 1 < nseg) cursor_next(p, ips, c);
+                }
+            }
+        }
+        if (p.k_new) {
+            // the append's rows are written by the first lanes of this wave
+            FlagOp no_flags;  // f16 pools keep no clamp flags
+            fused_append<VSPEC_KV_F16, D, false>(p, ws, first, ips, no_flags, nullptr);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // q rows loaded, appended rows stored
+#pragma unroll
+        for (int s = 0; s < kQStage; ++s) {
+            if (s < nseg) {
+#pragma unroll
+                for (int j = 0; j < QPL; ++j) {
+                    const int i = lane + 64 * j;
+                    if (i < GW * D) qraw[s][i / D][i % D] = qreg[s][j];
+                }
+            }
+        }
+        if (lane < kSlots) {
+            slot_cnt[lane] = 0;
+            slot_seg[lane] = lane;
         }
     }
+    if (!defer) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * kWaves, f[u]);
+    }
     __syncthreads();
+    if (defer) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * kWaves, f[u]);
+    }
     reset();
     qprep(0, pc);
     for (int k = 0; k < nt; k += NB) {
