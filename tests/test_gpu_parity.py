@@ -879,15 +879,19 @@ def test_decode_step_new_token_dominates(oracle, gpu, flag_gate, dtype):
 
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
 @pytest.mark.parametrize("B,T,pt", [(64, 4097, 0), (16, 2049, 0), (3, 300, 0), (8, 1025, 32), (8, 1024, 64)])
-def test_decode_min_ctx_len_hint(gpu, dtype, B, T, pt):
+def test_decode_min_ctx_len_hint(gpu, dtype, B, T, pt, monkeypatch):
     """min_ctx_len == max_ctx_len (every context the same) lets the host skip the merge
     launch when no work item spans two workgroups (64 x 4097: each workgroup holds whole
     items) and keeps it otherwise; the decode step's outputs and pool bytes equal those
-    without the hint bit for bit, with the balanced and the chunked split."""
+    without the hint bit for bit, with the balanced and the chunked split.  (The 8-wave
+    whole-item kernel, which the hint can also select, splits differently: switched off
+    here, tested against the oracle in test_decode_wide_whole_items.)"""
     import ctypes as C
 
     import torch
     import vspec_rocm as vr
+
+    monkeypatch.setenv("VSPEC_ROCM_DECODE_WIDE", "0")
 
     say(f"[min_ctx_len] dtype={dtype} B={B} T={T} pt={pt}")
     Hq, Hkv, D, P = 32, 8, 128, 16
@@ -916,6 +920,55 @@ def test_decode_min_ctx_len_hint(gpu, dtype, B, T, pt):
     for a, b in zip(pool_bytes(pools[0]), pool_bytes(pools[1])):
         if a is not None:
             assert np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,P,B,T", [
+    (128, 32, 8, 16, 32, 2049),   # 256 items of 129 tiles: the default rule picks it
+    (128, 32, 8, 16, 16, 2049),   # C2: 128 items
+    (128, 32, 8, 16, 1, 1025),    # one sequence, 8 items
+    (128, 16, 4, 32, 5, 300),     # GQA 4, 32-token blocks, a partial last tile
+    (64, 8, 8, 16, 7, 33),        # MHA, head_dim 64, three tiles per item
+    (128, 24, 2, 16, 3, 4100),    # GQA 12 (three q-head groups per kv head), 257 tiles
+    (64, 6, 2, 48, 4, 17),        # GQA 3, 48-token blocks, two tiles
+])
+def test_decode_wide_whole_items(oracle, gpu, D, Hq, Hkv, P, B, T, monkeypatch):
+    """f16 batches with every context the same (min_ctx_len == max_ctx_len) and about one
+    work item per CU run one whole item per workgroup of 8 waves (no merge launch); forced
+    here for smaller batches too (VSPEC_ROCM_DECODE_WIDE=2).  Against the oracle in both
+    numerics modes, through the plain decode and the fused decode step (whose appended rows
+    are bit-exact)."""
+    import torch
+    import vspec_rocm as vr
+
+    monkeypatch.setenv("VSPEC_ROCM_DECODE_WIDE", "2")
+    say(f"[wide] D={D} Hq={Hq} Hkv={Hkv} P={P} B={B} T={T}")
+    ctx = [T] * B
+    case = make_case(oracle, DTYPE_F16, B, Hq, Hkv, D, P, ctx, seed=11 * D + Hq + B + T)
+    pool = build_both(oracle, case, gpu)
+    tab = torch.from_numpy(case.tables).to(gpu)
+    cl = torch.from_numpy(case.ctx).to(gpu)
+    q = torch.from_numpy(case.q).to(gpu)
+    for mode in (0, 1):
+        out = vr.paged_decode(pool, tab, cl, q, max_ctx_len=T, numerics=mode, min_ctx_len=T)
+        torch.cuda.synchronize()
+        check_attention(oracle, case, out.cpu().numpy(), mode)
+    # fused step: the same stream minus its last token, which the decode step appends
+    import copy
+
+    pre = copy.copy(case)
+    pre.ctx = (case.ctx - 1).astype(np.int32)
+    pre.host = HostPool(DTYPE_F16, case.num_blocks, P, Hkv, D)
+    fill_garbage(pre.host)
+    pool2 = build_both(oracle, pre, gpu)
+    k_new = np.ascontiguousarray(case.k_tokens[:, T - 1])  # [B][Hkv][D]
+    v_new = np.ascontiguousarray(case.v_tokens[:, T - 1])
+    assert oracle.paged_append(pre.host, case.tables, pre.ctx, np.ascontiguousarray(k_new[:, None]),
+                               np.ascontiguousarray(v_new[:, None]))
+    got = vr.paged_decode_step(pool2, tab, cl, q, _np_to_dev(k_new, gpu), _np_to_dev(v_new, gpu), max_ctx_len=T,
+                               numerics=1, min_ctx_len=T)
+    torch.cuda.synchronize()
+    assert_pools_equal(pre.host, pool2)
+    check_attention(oracle, case, got.cpu().numpy(), 1)
 
 
 def test_graph_replay_survives_workspace_growth(oracle, gpu):

@@ -44,24 +44,24 @@ struct Frags {
 // item boundaries: the ring's loads run NB tiles ahead on their own cursor, and where
 // the processed tiles enter a new work item the wave hands its softmax state for the
 // old one to an LDS merge slot, resets it and prepares the new item's q operands from
-// q rows staged in LDS up front.  The last of the four waves to hand in an item's state
-// merges the four; no barrier stops the ring.
-template <int D, int GW, int PB, int NB, bool USED>
-__global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
+// q rows staged in LDS up front.  The last of the waves to hand in an item's state
+// merges them all; no barrier stops the ring.
+template <int D, int GW, int PB, int NB, bool USED, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams p) {
     constexpr int NQK = D / 32;   // QK MFMAs per tile (each on 32 d)
     constexpr int NDT = D / 16;   // PV d-tiles
     constexpr int kQStage = 4;    // item segments whose q rows are staged up front
     constexpr int kSlots = 2;     // item segments being merged at once
     __shared__ float qraw[kQStage][GW][D];
-    __shared__ float qs[kWaves][GW][D];  // per wave: q' of its current item
+    __shared__ float qs[NW][GW][D];  // per wave: q' of its current item
     // per wave: QK B operands (hi, lo for each 32-wide d chunk), read back every tile
-    __shared__ uint4 qb_lds[kWaves][NQK][2][64];
-    __shared__ float comb[kSlots][kWaves][GW][D + 2];
-    __shared__ float patch_val[kWaves][kTile][4];
-    __shared__ int patch_flag[kWaves][kTile];
+    __shared__ uint4 qb_lds[NW][NQK][2][64];
+    __shared__ float comb[kSlots][NW][GW][D + 2];
+    __shared__ float patch_val[NW][kTile][4];
+    __shared__ int patch_flag[NW][kTile];
     __shared__ int slot_cnt[kSlots];
     __shared__ int slot_seg[kSlots];
-    __shared__ SplitShared split_sh;
+    __shared__ SplitSharedN<NW> split_sh;
 
     const int lane = threadIdx.x & 63;
     // wave index as a scalar: tile loop control and block-table reads stay on the
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     const int n = lane & 15;   // column / token within the tile
 
     const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
-    const WorkSplit ws = work_split<kSplitRagged>(p, ips, split_sh);
+    const WorkSplit ws = work_split<kSplitRagged, NW>(p, ips, split_sh);
     if (ws.lo >= ws.hi) return;
     const ItemCursor first = cursor_at(p, ws);
 
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     };
 
     // Hand this wave's state for segment s (work item c) to merge slot s % kSlots; the
-    // last of the kWaves waves to hand in merges the four states.  A slot serves segment
+    // last of the NW waves to hand in merges their states.  A slot serves segment
     // s once segment s - kSlots is merged; waves hand in segments in order, so the wave
     // furthest behind never waits here and every wait ends.
     auto arrive = [&](const int s, const ItemCursor& c) {
@@ -361,10 +361,10 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
         int before = 0;
         if (lane == 0) before = __hip_atomic_fetch_add(&slot_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         before = __builtin_amdgcn_readfirstlane(before);
-        if (before == kWaves - 1) {
+        if (before == NW - 1) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             const bool whole = c.item0 >= ws.lo && c.item0 + c.U <= ws.hi;
-            merge_segment<D, GW>(p, comb[slot], lane, (size_t)c.b * p.hq + (size_t)c.y * GW, whole, s == 0 ? 0 : 1);
+            merge_segment<D, GW, NW>(p, comb[slot], lane, (size_t)c.b * p.hq + (size_t)c.y * GW, whole, s == 0 ? 0 : 1);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             if (lane == 0) {
                 slot_cnt[slot] = 0;
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     int pctx = min(max(as_const(p.ctx_lens)[pc.b], 0), ctx_cap);
     const int len = ws.hi - ws.lo;
     const int t0 = ws.lo + wave;
-    const int nt = wave < len ? (len - wave + kWaves - 1) / kWaves : 0;
+    const int nt = wave < len ? (len - wave + NW - 1) / NW : 0;
     Frags<D> f[NB];
     int ok[NB];
     // Set-up.  Wave 0 loads the q rows of the range's first kQStage segments (rows GW*y ..
@@ -399,10 +399,10 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     bool defer = false;
     if (p.k_new && wave != 0) {
         ItemCursor c = first;
-        const int end = min(ws.hi, ws.lo + NB * kWaves);
+        const int end = min(ws.hi, ws.lo + NB * NW);
         while (true) {
             const int last = c.item0 + c.U - 1;
-            if (last >= ws.lo && last < end && (last - ws.lo) % kWaves == wave) defer = true;
+            if (last >= ws.lo && last < end && (last - ws.lo) % NW == wave) defer = true;
             if (c.item0 + c.U >= end) break;
             cursor_next(p, ips, c);
         }
@@ -455,19 +455,19 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
     }
     if (!defer) {
 #pragma unroll
-        for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * kWaves, f[u]);
+        for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * NW, f[u]);
     }
     __syncthreads();
     if (defer) {
 #pragma unroll
-        for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * kWaves, f[u]);
+        for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * NW, f[u]);
     }
     reset();
     qprep(0, pc);
     for (int k = 0; k < nt; k += NB) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            const int t = t0 + (k + u) * kWaves;
+            const int t = t0 + (k + u) * NW;
             if (t < ws.hi && t >= pc.item0 + pc.U) {
                 do {
                     arrive(seg, pc);
@@ -479,7 +479,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
                 qprep(seg, pc);
             }
             process(f[u], ok[u], t - pc.item0, pctx);
-            ok[u] = load(t + NB * kWaves, f[u]);
+            ok[u] = load(t + NB * NW, f[u]);
         }
     }
     // hand in the current segment and every later one of the workgroup (empty states)
@@ -499,10 +499,17 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_f16(DecodeParams p) {
 template <int D, int GW, bool USED>
 void launch_used(const DecodeParams& p, dim3 grid, hipStream_t s) {
     constexpr int NB = VSPEC_F16_TILES_IN_FLIGHT;
-    if (p.block_tokens == 16) {
-        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 16, NB, USED>), grid, dim3(256), 0, s, p);
+    if (p.wide) {
+        // one work item per workgroup of 8 waves (no item spans two workgroups)
+        if (p.block_tokens == 16) {
+            hipLaunchKernelGGL((decode_mfma_f16<D, GW, 16, NB, USED, 8>), grid, dim3(512), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0, NB, USED, 8>), grid, dim3(512), 0, s, p);
+        }
+    } else if (p.block_tokens == 16) {
+        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 16, NB, USED, kWaves>), grid, dim3(256), 0, s, p);
     } else {
-        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0, NB, USED>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((decode_mfma_f16<D, GW, 0, NB, USED, kWaves>), grid, dim3(256), 0, s, p);
     }
 }
 

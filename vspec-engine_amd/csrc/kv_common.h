@@ -226,6 +226,9 @@ struct DecodeParams {
     // tiles per work item when the host knows every context to be the same (min_ctx_len ==
     // max_ctx_len), else 0: the split then needs no pass over ctx_lens
     uint32_t uniform_tiles;
+    // f16 pools: workgroups of 8 waves, each taking whole work items (chunk_tiles is a
+    // multiple of the uniform tiles per item), for batches with few, short items
+    bool wide;
 };
 
 // Launch the MFMA decode kernels for f16 pools (decode_mfma.hip) and int4 pools
@@ -311,14 +314,16 @@ struct WorkSplit {
     int seq0;    // index of that sequence's first tile
 };
 
-struct SplitShared {
-    int wsum[kWaves];
-    int umin[kWaves];  // per wave: least and greatest tiles per work item (U_b)
-    int umax[kWaves];
-    int wpre[kWaves];  // merge launch: per wave, tiles of the sequences before the item's
+template <int NW>
+struct SplitSharedN {
+    int wsum[NW];
+    int umin[NW];  // per wave: least and greatest tiles per work item (U_b)
+    int umax[NW];
+    int wpre[NW];  // merge launch: per wave, tiles of the sequences before the item's
     int b;
     int seq0;
 };
+using SplitShared = SplitSharedN<kWaves>;
 
 __device__ __forceinline__ int item_tiles(const DecodeParams& p, int b) {
     if (p.uniform_tiles) return (int)p.uniform_tiles;
@@ -401,10 +406,10 @@ __device__ __forceinline__ void split_range(const DecodeParams& p, WorkSplit& r)
     }
 }
 
-// Block-wide (every thread calls it; the result is uniform).  The host keeps
+// Block-wide over NW waves (every thread calls it; the result is uniform).  The host keeps
 // T = hkv * gsplit * sum U_b below 2^31.
-template <int UNEVEN>
-__device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, SplitShared& sh) {
+template <int UNEVEN, int NW = kWaves>
+__device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, SplitSharedN<NW>& sh) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nb = (int)p.batch;
@@ -419,7 +424,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         r.seq0 = r.b * per_seq;
         return r;
     }
-    if (nb <= kWaves * 64) {
+    if (nb <= NW * 64) {
         // one sequence per thread: the total and the search come from one scan
         const int b = (int)threadIdx.x;
         const int u = b < nb ? item_tiles(p, b) : 0;
@@ -447,7 +452,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         umin = 0x7fffffff;
         umax = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             before += w < wave ? sh.wsum[w] : 0;
             all += sh.wsum[w];
             if constexpr (UNEVEN == kSplitRagged) {
@@ -472,7 +477,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         return r;
     }
     int s = 0, umin = 0x7fffffff, umax = 0;
-    for (int b = threadIdx.x; b < nb; b += kWaves * 64) {
+    for (int b = threadIdx.x; b < nb; b += NW * 64) {
         const int u = item_tiles(p, b);
         s += u;
         if constexpr (UNEVEN == kSplitRagged) {
@@ -498,7 +503,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
     umin = 0x7fffffff;
     umax = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
         units += sh.wsum[w];
         umin = min(umin, sh.umin[w]);
         umax = max(umax, sh.umax[w]);
@@ -511,7 +516,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
     if (r.lo >= r.hi) return r;
     // the sequence holding tile lo: exclusive prefix of U_b * ips, 256 sequences a pass
     int carry = 0;
-    for (int base = 0; base < nb; base += kWaves * 64) {
+    for (int base = 0; base < nb; base += NW * 64) {
         const int b = base + (int)threadIdx.x;
         const int u = b < nb ? item_tiles(p, b) : 0;
         int x = u;
@@ -525,7 +530,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         __syncthreads();
         int before = 0, all = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             before += w < wave ? sh.wsum[w] : 0;
             all += sh.wsum[w];
         }
@@ -577,10 +582,10 @@ __device__ __forceinline__ void cursor_next(const DecodeParams& p, int ips, Item
     }
 }
 
-// One wave merges the kWaves states of one item segment held in LDS (st[w][h] =
-// {max, sum, acc[D]}, written by wave w) and writes the output rows of a whole work
-// item, or else the workgroup's partial `pslot` (0: its first segment, 1: its last).
-template <int D, int GW>
+// One wave merges the NW states of one item segment held in LDS (st[w][h] = {max, sum,
+// acc[D]}, written by wave w) and writes the output rows of a whole work item, or else the
+// workgroup's partial `pslot` (0: its first segment, 1: its last).
+template <int D, int GW, int NW = kWaves>
 __device__ __forceinline__ void merge_segment(const DecodeParams& p, const float (*st)[GW][D + 2], int lane,
                                               size_t row0, bool whole, int pslot) {
     float* pacc = p.part_acc + ((size_t)blockIdx.x * 2 + pslot) * GW * D;
@@ -590,10 +595,10 @@ __device__ __forceinline__ void merge_segment(const DecodeParams& p, const float
         const int d = idx % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int v = 0; v < kWaves; ++v) M = fmaxf(M, st[v][h][0]);
+        for (int v = 0; v < NW; ++v) M = fmaxf(M, st[v][h][0]);
         float a = 0.f, l = 0.f;
 #pragma unroll
-        for (int v = 0; v < kWaves; ++v) {
+        for (int v = 0; v < NW; ++v) {
             const float f = exp2f(st[v][h][0] - M);
             a = fmaf(st[v][h][2 + d], f, a);
             l = fmaf(st[v][h][1], f, l);

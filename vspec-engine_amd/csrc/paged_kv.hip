@@ -789,6 +789,21 @@ uint32_t decode_min_tiles_per_wg(uint64_t items) {
     return items <= 8 ? 16u : 1u;
 }
 
+// f16 batches whose contexts the host knows to be the same, whose work items about fill the
+// CUs (between 15/16 of them and all of them) and hold at least 96 tiles each run one whole
+// item per workgroup of 8 waves instead of splitting items over workgroups and merging
+// their partial states in a second launch.  VSPEC_ROCM_DECODE_WIDE (read on every call): 0
+// never, 2 whenever the items fit the CUs, else (default, 1) the rule above.  Measured at
+// B = 32 (256 items), whole against split: 1025 tokens 33.6 / 32.3 us, 2049 53.9 / 57.4,
+// 4097 94.0 / 97.6, 8193 174.1 / 177.4, 32769 665 / 669; B = 30 at 4097: 90.4 / 97.1.
+// With fewer items the split over all CUs wins (C2, 128 items: 36.0 split, 44.0 whole).
+bool decode_wide(uint64_t items, uint64_t cus, uint64_t tiles) {
+    const char* e = getenv("VSPEC_ROCM_DECODE_WIDE");
+    const long x = e ? strtol(e, nullptr, 10) : 1;
+    if (x == 0 || items > cus) return false;
+    return x == 2 || (items * 16 >= cus * 15 && tiles >= 96);
+}
+
 // int4 clamp flags are read by the decode only when the balanced split gives each workgroup
 // at least this many tiles (VSPEC_ROCM_DECODE_FLAG_MIN_TILES, 0..4096); shorter shares read
 // no flags and screen every tile.  Read on every call.
@@ -801,6 +816,7 @@ uint32_t decode_flag_min_tiles() {
 
 struct DecodePlan {
     bool merge;  // split MFMA kernels: some work item may span two workgroups (merge launch)
+    bool wide;   // f16: one whole work item per workgroup of 8 waves (no merge launch)
     uint32_t gw;
     uint32_t gsplit;
     uint32_t tiles_per_part;
@@ -889,6 +905,7 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
     }
     const uint32_t max_tiles = (uint32_t)((ctx_bound + kTile - 1) / kTile);
     pl->split = d->kv.dtype != VSPEC_KV_F32;
+    pl->wide = false;
     pl->min_tiles = decode_min_tiles_per_wg((uint64_t)d->batch * hkv * pl->gsplit);
     if (pl->split) {
         // every workgroup streams an equal share of all work items' tiles
@@ -905,6 +922,13 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
             }
             pl->chunk_tiles = d->partition_tokens / kTile;
             grid = (bound + pl->chunk_tiles - 1) / pl->chunk_tiles;
+        } else if (d->kv.dtype == VSPEC_KV_F16 && d->min_ctx_len && d->min_ctx_len >= ctx_bound &&
+                   decode_wide((uint64_t)d->batch * hkv * pl->gsplit, (uint64_t)num_cus(), max_tiles)) {
+            // whole items on 8-wave workgroups: every context is the same (the host says so),
+            // so chunks of one item's tiles are exactly the items
+            pl->wide = true;
+            pl->chunk_tiles = 0;  // set below from the items' tiles
+            grid = (uint64_t)d->batch * hkv * pl->gsplit;
         } else {
             pl->chunk_tiles = 0;
             // two workgroups per CU; small f16 batches (under 64 tiles per workgroup at two
@@ -926,6 +950,7 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
         // unequal pair shares need the grid of two workgroups per CU (g and g + G/2 share one)
         pl->old_permille = !pl->chunk_tiles && pl->grid_x == 2u * (uint32_t)num_cus()
                                ? decode_old_permille(d->kv.dtype) : 500u;
+        if (pl->wide) pl->chunk_tiles = uniform_item_tiles(d, pl, ctx_bound);
         pl->merge = uniform_split_has_partials(d, pl, ctx_bound);
         pl->uniform_tiles = uniform_item_tiles(d, pl, ctx_bound);
         // the workspace stays even without a merge launch: a context below min_ctx_len (a
@@ -1435,6 +1460,7 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.split_old_permille = pl.split ? pl.old_permille : 500u;
     p.uniform_tiles = pl.split ? pl.uniform_tiles : 0u;
     p.min_tiles = pl.split && !pl.chunk_tiles ? pl.min_tiles : 1u;
+    p.wide = pl.wide;
 
     hipStream_t s = (hipStream_t)desc->stream;
     if (k_new) {

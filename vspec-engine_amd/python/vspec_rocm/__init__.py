@@ -486,9 +486,10 @@ def paged_decode(pool: PagedPool, block_tables, ctx_lens, q, max_ctx_len=None, n
 
 def paged_decode_step(pool: PagedPool, block_tables, ctx_lens, q, k_new, v_new, max_ctx_len=None,
                       numerics=NUMERICS_PLAIN, scale=0.0, partition_tokens=0, out=None, workspace=None,
-                      stream=None, block_used=None):
+                      stream=None, block_used=None, min_ctx_len=0):
     """vspec_rocm_paged_decode_step: append k_new / v_new [B][Hkv][D] (float32 or float16,
-    device) at position ctx_lens[b] - 1, then decode q [B][Hq][D] float32 -> out."""
+    device) at position ctx_lens[b] - 1, then decode q [B][Hq][D] float32 -> out.
+    min_ctx_len: the host's lower bound on ctx_lens (0: none)."""
     import torch
 
     assert q.dtype == torch.float32 and q.is_contiguous()
@@ -503,7 +504,8 @@ def paged_decode_step(pool: PagedPool, block_tables, ctx_lens, q, k_new, v_new, 
         max_ctx_len = int(cl.max().item()) if cl.numel() else 0
     if out is None:
         out = torch.empty_like(q)
-    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream, bu)
+    d = make_decode_desc(pool, bt, cl, q, out, max_ctx_len, numerics, scale, partition_tokens, workspace, stream, bu,
+                         min_ctx_len)
     _check(lib().vspec_rocm_paged_decode_step(C.byref(d), k_new.data_ptr(), v_new.data_ptr(), src),
            "paged_decode_step")
     _hold(stream, bt, cl, bu, out)
