@@ -35,6 +35,113 @@ struct Frags {
     uint2 v[D / 16];  // V^T row d = 16j + n, slots 4g .. 4g+3 of the tile
 };
 
+// Fused decode-step append for f16 pools, run by one wave: the token rows of every work
+// item whose last tile lies in the range [ws.lo, ws.hi) (c: the item holding ws.lo), which
+// exactly one workgroup covers.  Lanes take (item, 8-element chunk of K or V) pairs, IPP
+// items per pass and PASSES passes per round, and all loads of a round go out before its
+// stores: the items' contexts and source chunks together, then their table entries.  The
+// bytes written are those of append_chunk<VSPEC_KV_F16> (a copy of f16 source bits, or the
+// round-to-nearest-even conversion of f32 ones), so a range with many short items costs a
+// few load round trips instead of one chain of dependent loads and stores per item.
+template <int D>
+__device__ void fused_append_f16(const DecodeParams& p, const WorkSplit& ws, ItemCursor c, const int ips,
+                                 const int lane) {
+    constexpr int CH = D / 8;       // 8-element chunks per row
+    constexpr int LPI = 2 * CH;     // lanes per item: K chunks, then V chunks
+    constexpr int IPP = 64 / LPI;   // items per pass
+    constexpr int PASSES = 8;
+    static_assert(64 % LPI == 0, "items per pass");
+    const int chunk = (lane % LPI) % CH;
+    const int which = (lane % LPI) / CH;  // 0: K, 1: V
+    const int my = lane / LPI;            // this lane's item slot in a pass
+    const bool f32src = p.append_src == VSPEC_KV_F32;
+    bool done = false;
+    while (!done) {
+        int ib[PASSES], ih[PASSES];  // per pass: this lane's sequence (-1: none) and kv head
+#pragma unroll
+        for (int k = 0; k < PASSES; ++k) {
+            ib[k] = -1;
+            ih[k] = 0;
+#pragma unroll
+            for (int i = 0; i < IPP; ++i) {
+                int fb = -1, fh = 0;
+                while (!done) {
+                    const int last = c.item0 + c.U - 1;
+                    const bool mine = last >= ws.lo && last < ws.hi;
+                    const int cb = c.b, chk = c.y / (int)p.gsplit;
+                    if (c.item0 + c.U >= ws.hi) done = true;
+                    else cursor_next(p, ips, c);
+                    if (mine) {
+                        fb = cb;
+                        fh = chk;
+                        break;
+                    }
+                }
+                if (my == i) {
+                    ib[k] = fb;
+                    ih[k] = fh;
+                }
+            }
+        }
+        int ctx[PASSES];
+        uint4 s0[PASSES], s1[PASSES];
+#pragma unroll
+        for (int k = 0; k < PASSES; ++k) {
+            ctx[k] = 0;
+            if (ib[k] >= 0) {
+                ctx[k] = p.ctx_lens[ib[k]];
+                const size_t el = ((size_t)ib[k] * p.hkv + ih[k]) * D + (size_t)chunk * 8;
+                const uint8_t* src = which ? p.v_new : p.k_new;
+                if (f32src) {
+                    s0[k] = *reinterpret_cast<const uint4*>(src + el * 4);
+                    s1[k] = *reinterpret_cast<const uint4*>(src + el * 4 + 16);
+                } else {
+                    s0[k] = *reinterpret_cast<const uint4*>(src + el * 2);
+                }
+            }
+        }
+        int ent[PASSES];
+#pragma unroll
+        for (int k = 0; k < PASSES; ++k) {
+            ent[k] = -1;
+            if (ib[k] >= 0 && ctx[k] > 0) {
+                const uint32_t lb = (uint32_t)(ctx[k] - 1) / p.block_tokens;
+                if (lb < p.max_blocks) ent[k] = p.block_tables[(size_t)ib[k] * p.max_blocks + lb];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < PASSES; ++k) {
+            if (ent[k] < 0 || (uint32_t)ent[k] >= p.num_blocks) continue;
+            const uint32_t slot = (uint32_t)(ctx[k] - 1) % p.block_tokens;
+            const size_t bh = (size_t)ent[k] * p.hkv + ih[k];
+            uint32_t hb[8];
+            if (f32src) {
+                const float xs[8] = {__uint_as_float(s0[k].x), __uint_as_float(s0[k].y), __uint_as_float(s0[k].z),
+                                     __uint_as_float(s0[k].w), __uint_as_float(s1[k].x), __uint_as_float(s1[k].y),
+                                     __uint_as_float(s1[k].z), __uint_as_float(s1[k].w)};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hb[e] = float_to_half_bits(xs[e]);
+            } else {
+                const uint32_t ws4[4] = {s0[k].x, s0[k].y, s0[k].z, s0[k].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    hb[2 * e] = ws4[e] & 0xffffu;
+                    hb[2 * e + 1] = ws4[e] >> 16;
+                }
+            }
+            if (which) {
+                // V tiles are d-major: element (d, slot) at tile + d*P + slot
+                uint16_t* vt = reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(p.v)) + bh * D * p.block_tokens + slot;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vt[(size_t)(chunk * 8 + e) * p.block_tokens] = (uint16_t)hb[e];
+            } else {
+                *reinterpret_cast<uint4*>(const_cast<uint8_t*>(p.k) + ((bh * p.block_tokens + slot) * D + chunk * 8) * 2) =
+                    make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16), hb[6] | (hb[7] << 16));
+            }
+        }
+    }
+}
+
 // PB: block_tokens known at compile time (16), or 0 for any multiple of 16;
 // NB: tiles in flight per wave; USED: per-block used counts cap each tile (block_used)
 //
@@ -432,11 +539,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
                 }
             }
         }
-        if (p.k_new) {
-            // the append's rows are written by the first lanes of this wave
-            FlagOp no_flags;  // f16 pools keep no clamp flags
-            fused_append<VSPEC_KV_F16, D, false>(p, ws, first, ips, no_flags, nullptr);
-        }
+        if (p.k_new) fused_append_f16<D>(p, ws, first, ips, lane);
         __builtin_amdgcn_s_waitcnt(0);  // q rows loaded, appended rows stored
 #pragma unroll
         for (int s = 0; s < kQStage; ++s) {

@@ -229,6 +229,9 @@ struct DecodeParams {
     // f16 pools: workgroups of 8 waves, each taking whole work items (chunk_tiles is a
     // multiple of the uniform tiles per item), for batches with few, short items
     bool wide;
+    // balanced split of a ragged batch: each work item also costs this many tiles (its
+    // set-up and merge in every workgroup that starts it), 0: tiles only
+    uint32_t seg_cost;
 };
 
 // Launch the MFMA decode kernels for f16 pools (decode_mfma.hip) and int4 pools
@@ -283,7 +286,12 @@ __device__ __forceinline__ void merge_waves(const DecodeParams& p, const float (
 // a sequence adjacent, T tiles in all.  Workgroup g takes the tiles [lo_g, lo_{g+1}):
 //   balanced  lo_g = floor(g * T / G), G = min(split_grid, T)
 //   chunked   lo_g = g * chunk_tiles
-// so every workgroup streams the same number of tiles whatever the context lengths.
+// so every workgroup streams the same number of tiles whatever the context lengths.  In
+// a ragged batch each work item can also cost alpha tiles (DecodeParams.seg_cost): the
+// split then runs over a cost axis on which item i occupies [c_i, c_i + alpha + U_i)
+// (c_i = its first tile + alpha * i), alpha units of set-up followed by its tiles, and a
+// workgroup's cost range maps back to the tiles it covers (a boundary inside an item's
+// set-up units falls on its first tile).
 // A work item that lies inside one workgroup's range goes straight to the output; one
 // that spans several leaves one partial (max, sum, acc) per workgroup, in slot 0 when
 // it is that workgroup's first segment and slot 1 when its last.  A second launch on the
@@ -304,7 +312,9 @@ constexpr int kSplitRagged = 1;
 constexpr int kSplitAlways = 2;
 
 struct WorkSplit {
-    int total;   // T
+    int total;   // T (balanced split with a segment cost: tiles plus alpha per work item)
+    int tiles;   // tiles of all work items
+    int alpha;   // cost of a work item in tiles on top of its own (0: none)
     int groups;  // G (balanced split), 0 for the chunked split
     int half;    // G / 2 when the two halves of the grid get different shares, else 0
     int wa;      // share of a first-half workgroup in a (first, second) pair, in 1/1000
@@ -322,6 +332,7 @@ struct SplitSharedN {
     int wpre[NW];  // merge launch: per wave, tiles of the sequences before the item's
     int b;
     int seq0;
+    int lo_t, hi_t;  // balanced split with a segment cost: the range in tiles
 };
 using SplitShared = SplitSharedN<kWaves>;
 
@@ -363,6 +374,20 @@ __device__ __forceinline__ int split_group_of(const DecodeParams& p, const WorkS
     const long long g = (n - 1) / a;
     if (g < w.half) return (int)g;
     return w.half + (int)((n - a * w.half - 1) / ((long long)(1000 - w.wa) * w.total));
+}
+
+// Tile position of cost position xc inside sequence b, whose tiles start at tile ex_t and
+// cost unit ex_c, with u tiles per work item (the cost axis of work_split).
+__device__ __forceinline__ int cost_to_tile(int xc, int ex_t, int ex_c, int u, int alpha) {
+    const int d = xc - ex_c;
+    const int k = d / (u + alpha);
+    const int off = d - k * (u + alpha);
+    return ex_t + k * u + min(max(off - alpha, 0), u);
+}
+
+// alpha of a split: the segment cost applies to ragged batches under the balanced split
+__device__ __forceinline__ int split_alpha(const DecodeParams& p, int ragged) {
+    return p.seg_cost && ragged && !p.chunk_tiles ? (int)p.seg_cost : 0;
 }
 
 // The split's shape once T (and whether the batch is ragged) is known: groups and pair
@@ -418,6 +443,8 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         // every sequence holds uniform_tiles tiles per work item: no scan, no barrier
         const int per_seq = (int)p.uniform_tiles * ips;
         r.total = nb * per_seq;
+        r.tiles = r.total;
+        r.alpha = 0;
         r.ragged = 0;
         split_range<UNEVEN>(p, r);
         r.b = r.lo < r.hi ? r.lo / per_seq : 0;
@@ -460,13 +487,34 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
                 umax = max(umax, sh.umax[w]);
             }
         }
-        r.total = __builtin_amdgcn_readfirstlane(all) * ips;
+        r.tiles = __builtin_amdgcn_readfirstlane(all) * ips;
         r.ragged = UNEVEN == kSplitRagged ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
+        r.alpha = split_alpha(p, r.ragged);
+        r.total = r.tiles + r.alpha * ips * nb;
         split_range<UNEVEN>(p, r);
         r.b = 0;
         r.seq0 = 0;
         if (r.lo >= r.hi) return r;
         const int excl = (before + x - u) * ips;
+        if (r.alpha) {
+            // cost range -> tiles: the sequences holding its ends map them
+            const int ex_c = excl + r.alpha * ips * b;
+            const int span = ips * (u + r.alpha);
+            if (u > 0 && ex_c <= r.lo && r.lo < ex_c + span) {
+                sh.lo_t = cost_to_tile(r.lo, excl, ex_c, u, r.alpha);
+                sh.b = b;
+                sh.seq0 = excl;
+            }
+            if (u > 0 && ex_c <= r.hi && r.hi < ex_c + span) sh.hi_t = cost_to_tile(r.hi, excl, ex_c, u, r.alpha);
+            __syncthreads();
+            const int lo_t = r.lo < r.total ? __builtin_amdgcn_readfirstlane(sh.lo_t) : r.tiles;
+            const int hi_t = r.hi < r.total ? __builtin_amdgcn_readfirstlane(sh.hi_t) : r.tiles;
+            r.b = __builtin_amdgcn_readfirstlane(sh.b);
+            r.seq0 = __builtin_amdgcn_readfirstlane(sh.seq0);
+            r.lo = lo_t;
+            r.hi = hi_t;
+            return r;
+        }
         if (u > 0 && excl <= r.lo && r.lo < excl + u * ips) {
             sh.b = b;
             sh.seq0 = excl;
@@ -508,8 +556,10 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         umin = min(umin, sh.umin[w]);
         umax = max(umax, sh.umax[w]);
     }
-    r.total = __builtin_amdgcn_readfirstlane(units) * ips;
+    r.tiles = __builtin_amdgcn_readfirstlane(units) * ips;
     r.ragged = UNEVEN == kSplitRagged ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
+    r.alpha = split_alpha(p, r.ragged);
+    r.total = r.tiles + r.alpha * ips * nb;
     split_range<UNEVEN>(p, r);
     r.b = 0;
     r.seq0 = 0;
@@ -535,7 +585,16 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
             all += sh.wsum[w];
         }
         const int excl = (carry + before + x - u) * ips;
-        if (u > 0 && excl <= r.lo && r.lo < excl + u * ips) {
+        if (r.alpha) {
+            const int ex_c = excl + r.alpha * ips * b;
+            const int span = ips * (u + r.alpha);
+            if (u > 0 && ex_c <= r.lo && r.lo < ex_c + span) {
+                sh.lo_t = cost_to_tile(r.lo, excl, ex_c, u, r.alpha);
+                sh.b = b;
+                sh.seq0 = excl;
+            }
+            if (u > 0 && ex_c <= r.hi && r.hi < ex_c + span) sh.hi_t = cost_to_tile(r.hi, excl, ex_c, u, r.alpha);
+        } else if (u > 0 && excl <= r.lo && r.lo < excl + u * ips) {
             sh.b = b;
             sh.seq0 = excl;
         }
@@ -544,6 +603,12 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
     __syncthreads();
     r.b = __builtin_amdgcn_readfirstlane(sh.b);
     r.seq0 = __builtin_amdgcn_readfirstlane(sh.seq0);
+    if (r.alpha) {
+        const int lo_t = r.lo < r.total ? __builtin_amdgcn_readfirstlane(sh.lo_t) : r.tiles;
+        const int hi_t = r.hi < r.total ? __builtin_amdgcn_readfirstlane(sh.hi_t) : r.tiles;
+        r.lo = lo_t;
+        r.hi = hi_t;
+    }
     return r;
 }
 
@@ -660,12 +725,13 @@ __device__ __forceinline__ void finish_segment(const DecodeParams& p, const floa
 // groups and pair shares), and for an item whose tiles meet the ranges of workgroups
 // g0 < g1 it merges their partials in order g0..g1 and writes the item's output rows;
 // items inside one range were written by the split kernel and are left alone.  Partial
-// loads go out NBATCH workgroups at a time, all in flight together.
+// loads go out NBATCH workgroups at a time, all in flight together.  With uniform_tiles
+// (every context the same) the split needs no pass over ctx_lens.
 template <int D, int GW, int UNEVEN>
 __global__ __launch_bounds__(kWaves * 64) void decode_merge_split(DecodeParams p) {
     constexpr int NT = kWaves * 64;
     constexpr int K = (GW * D + NT - 1) / NT;  // outputs per thread: idx = tid + NT * k
-    constexpr int NBATCH = 8;
+    constexpr int NBATCH = 16;
     __shared__ SplitShared sh;
     const int ips = (int)(p.hkv * p.gsplit);
     const int b = (int)blockIdx.x / ips;
@@ -673,52 +739,65 @@ __global__ __launch_bounds__(kWaves * 64) void decode_merge_split(DecodeParams p
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nb = (int)p.batch;
-    // T, ragged and the tiles of the sequences before b, block-wide
-    int s = 0, pre = 0, umin = 0x7fffffff, umax = 0;
-    for (int i = threadIdx.x; i < nb; i += NT) {
-        const int u = item_tiles(p, i);
-        s += u;
-        pre += i < b ? u : 0;
-        umin = min(umin, u);
-        umax = max(umax, u);
-    }
-#pragma unroll
-    for (int o = 32; o; o >>= 1) {
-        s += __shfl_xor(s, o);
-        pre += __shfl_xor(pre, o);
-        umin = min(umin, __shfl_xor(umin, o));
-        umax = max(umax, __shfl_xor(umax, o));
-    }
-    if (lane == 0) {
-        sh.wsum[wave] = s;
-        sh.wpre[wave] = pre;
-        sh.umin[wave] = umin;
-        sh.umax[wave] = umax;
-    }
-    __syncthreads();
     WorkSplit w;
-    int all = 0;
-    pre = 0;
-    umin = 0x7fffffff;
-    umax = 0;
+    int pre = 0;
+    if (p.uniform_tiles) {
+        w.total = nb * (int)p.uniform_tiles * ips;
+        w.ragged = 0;
+        pre = b * (int)p.uniform_tiles;
+        w.tiles = w.total;
+        w.alpha = 0;
+    } else {
+        // T, ragged and the tiles of the sequences before b, block-wide
+        int s = 0, umin = 0x7fffffff, umax = 0;
+        for (int i = threadIdx.x; i < nb; i += NT) {
+            const int u = item_tiles(p, i);
+            s += u;
+            pre += i < b ? u : 0;
+            umin = min(umin, u);
+            umax = max(umax, u);
+        }
 #pragma unroll
-    for (int v = 0; v < kWaves; ++v) {
-        all += sh.wsum[v];
-        pre += sh.wpre[v];
-        umin = min(umin, sh.umin[v]);
-        umax = max(umax, sh.umax[v]);
+        for (int o = 32; o; o >>= 1) {
+            s += __shfl_xor(s, o);
+            pre += __shfl_xor(pre, o);
+            umin = min(umin, __shfl_xor(umin, o));
+            umax = max(umax, __shfl_xor(umax, o));
+        }
+        if (lane == 0) {
+            sh.wsum[wave] = s;
+            sh.wpre[wave] = pre;
+            sh.umin[wave] = umin;
+            sh.umax[wave] = umax;
+        }
+        __syncthreads();
+        int all = 0;
+        pre = 0;
+        umin = 0x7fffffff;
+        umax = 0;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) {
+            all += sh.wsum[v];
+            pre += sh.wpre[v];
+            umin = min(umin, sh.umin[v]);
+            umax = max(umax, sh.umax[v]);
+        }
+        w.tiles = all * ips;
+        w.ragged = UNEVEN == kSplitRagged && umin != umax ? 1 : 0;
+        w.alpha = split_alpha(p, w.ragged);
+        w.total = w.tiles + w.alpha * ips * nb;
     }
-    w.total = all * ips;
-    w.ragged = UNEVEN == kSplitRagged && umin != umax ? 1 : 0;
     split_shape<UNEVEN>(p, w);
     const int U = item_tiles(p, b);
     const int item0 = pre * ips + y * U;
-    const int g0 = split_group_of<UNEVEN>(p, w, item0);
-    const int g1 = split_group_of<UNEVEN>(p, w, item0 + U - 1);
+    // the item on the split's axis: set-up units from c0, its first tile at c0 + alpha
+    const int c0 = item0 + w.alpha * (b * ips + y);
+    const int g0 = split_group_of<UNEVEN>(p, w, c0 + w.alpha);
+    const int g1 = split_group_of<UNEVEN>(p, w, c0 + w.alpha + U - 1);
     if (g0 == g1) return;  // written by the split kernel
     // the item is g0's last segment (slot 1) when g0's range starts before it, and the
     // first segment (slot 0) of every later workgroup
-    const int first_inside = split_lo<UNEVEN>(p, w, g0) < item0 ? 1 : 0;
+    const int first_inside = split_lo<UNEVEN>(p, w, g0) < c0 ? 1 : 0;
     const int tid = (int)threadIdx.x;
     // running merge per output in log2 units; -1e30 (not -inf) keeps exp2 finite
     float M[K], A[K], Ls[K];

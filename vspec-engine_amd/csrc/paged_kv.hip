@@ -804,6 +804,19 @@ bool decode_wide(uint64_t items, uint64_t cus, uint64_t tiles) {
     return x == 2 || (items * 16 >= cus * 15 && tiles >= 96);
 }
 
+// Balanced split of ragged f16 batches: every work item also costs this many tiles
+// (VSPEC_ROCM_DECODE_SEGMENT_COST, 0..64; 0: tiles only), the set-up of its q operands and
+// the merge of its waves' states in each workgroup that holds part of it.  Measured on C4
+// (64 sequences, contexts U[128, 8192]): workgroups ran ~2 us longer per work item they
+// started, so those holding many short items ended the launch; decode step with a cost of
+// 0 / 2 / 4 / 8 / 16 tiles: 183.1 / 179.1 / 177.6 / 175.3 / 174.9 us.  Read on every call.
+constexpr uint32_t kDefaultSegmentCost = 16;
+uint32_t decode_segment_cost() {
+    const char* e = getenv("VSPEC_ROCM_DECODE_SEGMENT_COST");
+    const long x = e ? strtol(e, nullptr, 10) : -1;
+    return x >= 0 && x <= 64 ? (uint32_t)x : kDefaultSegmentCost;
+}
+
 // int4 clamp flags are read by the decode only when the balanced split gives each workgroup
 // at least this many tiles (VSPEC_ROCM_DECODE_FLAG_MIN_TILES, 0..4096); shorter shares read
 // no flags and screen every tile.  Read on every call.
@@ -1461,6 +1474,7 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.uniform_tiles = pl.split ? pl.uniform_tiles : 0u;
     p.min_tiles = pl.split && !pl.chunk_tiles ? pl.min_tiles : 1u;
     p.wide = pl.wide;
+    p.seg_cost = desc->kv.dtype == VSPEC_KV_F16 && pl.split && !pl.chunk_tiles ? decode_segment_cost() : 0u;
 
     hipStream_t s = (hipStream_t)desc->stream;
     if (k_new) {
