@@ -971,6 +971,48 @@ def test_decode_wide_whole_items(oracle, gpu, D, Hq, Hkv, P, B, T, monkeypatch):
     check_attention(oracle, case, got.cpu().numpy(), 1)
 
 
+@pytest.mark.parametrize("seg_cost", [0, 3, 16, 64])
+def test_decode_ragged_segment_cost(oracle, gpu, seg_cost, monkeypatch):
+    """Ragged f16 batches split over a cost axis on which every work item also costs
+    seg_cost tiles (VSPEC_ROCM_DECODE_SEGMENT_COST): workgroup ranges start and end inside
+    items' set-up units and inside their tiles, some are empty, items meet many workgroups
+    or none.  Many short sequences beside long ones, GQA 4 and 8 (two q-head groups per kv
+    head), plain decode and fused decode step: every output against the oracle, the step's
+    appended rows bit-exact.  (Unequal pair shares need >= 64 tiles per workgroup: the
+    full-size C4 test covers them with the default cost.)"""
+    import copy
+
+    import torch
+    import vspec_rocm as vr
+
+    monkeypatch.setenv("VSPEC_ROCM_DECODE_SEGMENT_COST", str(seg_cost))
+    say(f"[segment cost] cost={seg_cost}")
+    ctx = np.array([1, 17, 3000, 16, 33, 5, 200, 64, 2, 1500, 48, 129, 7, 4100, 31, 90] * 2, np.int32)
+    for Hq in (32, 64):
+        case = make_case(oracle, DTYPE_F16, len(ctx), Hq, 8, 128, 16, ctx, seed=900 + seg_cost + Hq)
+        pre = copy.copy(case)
+        pre.ctx = (case.ctx - 1).astype(np.int32)
+        pre.host = HostPool(DTYPE_F16, case.num_blocks, 16, 8, 128)
+        fill_garbage(pre.host)
+        pool = build_both(oracle, pre, gpu)
+        B = len(ctx)
+        k_new = np.ascontiguousarray(case.k_tokens[np.arange(B), ctx - 1])
+        v_new = np.ascontiguousarray(case.v_tokens[np.arange(B), ctx - 1])
+        assert oracle.paged_append(pre.host, case.tables, pre.ctx, np.ascontiguousarray(k_new[:, None]),
+                                   np.ascontiguousarray(v_new[:, None]))
+        tab = torch.from_numpy(case.tables).to(gpu)
+        cl = torch.from_numpy(case.ctx).to(gpu)
+        q = torch.from_numpy(case.q).to(gpu)
+        got = vr.paged_decode_step(pool, tab, cl, q, _np_to_dev(k_new, gpu), _np_to_dev(v_new, gpu), numerics=1)
+        torch.cuda.synchronize()
+        assert_pools_equal(pre.host, pool)
+        case.host = pre.host
+        check_attention(oracle, case, got.cpu().numpy(), 1)
+        out = vr.paged_decode(pool, tab, cl, q, numerics=0)
+        torch.cuda.synchronize()
+        check_attention(oracle, case, out.cpu().numpy(), 0)
+
+
 def test_graph_replay_survives_workspace_growth(oracle, gpu):
     """A decode captured into a HIP graph with the library's own workspace; then an eager
     decode on the same stream that needs a larger workspace makes the library replace it.

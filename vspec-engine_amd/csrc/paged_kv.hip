@@ -809,8 +809,10 @@ bool decode_wide(uint64_t items, uint64_t cus, uint64_t tiles) {
 // the merge of its waves' states in each workgroup that holds part of it.  Measured on C4
 // (64 sequences, contexts U[128, 8192]): workgroups ran ~2 us longer per work item they
 // started, so those holding many short items ended the launch; decode step with a cost of
-// 0 / 2 / 4 / 8 / 16 tiles: 183.1 / 179.1 / 177.6 / 175.3 / 174.9 us.  Read on every call.
-constexpr uint32_t kDefaultSegmentCost = 16;
+// 0 / 2 / 4 / 8 / 12 / 16 / 24 / 32 tiles: 183.1 / 179.1 / 177.6 / 175.3 / 172.6 / 174.1 /
+// 176.6 / 180.0 us (another seed of the same distribution: 226.1 at 0, 197.0 at 16).  Read on
+// every call.
+constexpr uint32_t kDefaultSegmentCost = 12;
 uint32_t decode_segment_cost() {
     const char* e = getenv("VSPEC_ROCM_DECODE_SEGMENT_COST");
     const long x = e ? strtol(e, nullptr, 10) : -1;
