@@ -141,9 +141,11 @@ typedef struct VspecPagedAttnDesc {
      * full except the last, and ctx_lens[b] is the token count. */
     const int32_t* block_used;
     /* Optional host lower bound of ctx_lens (0: none).  When it equals max_ctx_len (every
-     * context the same) the host knows the work split exactly and skips the merge launch
-     * if no work item spans two workgroups (e.g. 64 x 4097 tokens on 256 CUs).  A context
-     * below a non-zero bound is a caller error (its output may be left unwritten). */
+     * context the same) the host knows the work split exactly: it skips the merge launch
+     * if no work item spans two workgroups (e.g. 64 x 4097 tokens on 256 CUs), and f16
+     * batches whose work items about fill the CUs run one whole item per 8-wave workgroup.
+     * A context below a non-zero bound is a caller error (its output may be left
+     * unwritten). */
     uint32_t min_ctx_len;
 } VspecPagedAttnDesc;
 
