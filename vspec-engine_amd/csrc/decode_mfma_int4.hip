@@ -14,8 +14,10 @@
 //     summing the four columns of each head (DPP row rotations) gives the scores.
 //   output  O^T[d][16 col] += V codes^T x P'^T     v_mfma_f32_16x16x32_f16
 //     over two tiles (32 tokens) per step.  P' = p * (V scale of the token's group of
-//     d), rounded once to fp16.  The V pool is stored in 16-token tiles whose lane
-//     chunks are half of these A operands.
+//     d), rounded once to fp16: column n carries head n%4 with the V scales of group
+//     n/4, so one P' serves every group and output column 4q + h is read for group q's
+//     d.  The V pool is stored in 16-token tiles whose lane chunks are half of these A
+//     operands.
 //
 // A nibble t (two's complement code c = (t ^ 8) - 8) becomes an exact fp16 through a
 // magic exponent, two codes per 32-bit operation, plus a bias that the MFMAs cancel
@@ -71,7 +73,7 @@ struct I4Frags {
     uint32_t v[NQ];       // V tile lane chunk (g, n)
     uint32_t ks_own;      // K scale of (token n, this lane's group), low 16 bits
     uint2 ks_col;         // K scales of tokens 4g..4g+3 for column group (n/4) % G
-    uint32_t vs[2 * NQ];  // V scales of tokens 4g..4g+3, token-major (G per token)
+    _Float16 vs[4];       // V scales of tokens 4g..4g+3 for column group (n/4) % G
     uint32_t flags;       // clamp flags of the tile's 16 keys (the same in every lane)
     uint32_t fword;       // index of that flag word (wave-uniform)
 };
@@ -294,12 +296,9 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 const uint2 c = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(&st.v[h][0]) + 8 * lane);
                 f.v[0] = c.x; f.v[1] = c.y;
             }
-            const uint4* vs = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(&st.sc[h][32]) + 8 * NG * g);
+            const _Float16* vs = reinterpret_cast<const _Float16*>(&st.sc[h][32]) + 4 * NG * g + col_group;
 #pragma unroll
-            for (int i = 0; i < NQ / 2; ++i) {
-                const uint4 w = vs[i];
-                f.vs[4 * i] = w.x; f.vs[4 * i + 1] = w.y; f.vs[4 * i + 2] = w.z; f.vs[4 * i + 3] = w.w;
-            }
+            for (int r = 0; r < 4; ++r) f.vs[r] = vs[r * NG];
         };
 
         const int step = 2 * kWaves;
@@ -393,10 +392,13 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // (the K-scale FMA subtracts it), so the score clip moves with it: clip_lo/hi hold
         // the clip bounds minus m_run; columns that hold no head clip to -inf (3-bit mode:
         // +-24*log2e).  The wave's first scored pair of a work item sets m_run outright.
+        // Columns n, n+4, n+8 and n+12 hold head n%4's scores (the same values), so each
+        // keeps the head's whole state.
         float m_run = 0.f;
         float l_run = 0.f;
-        float clip_hi = n < GW ? p.logit_clip : -INFINITY;
-        float clip_lo = n < GW ? -p.logit_clip : -INFINITY;
+        const bool head_col = (n & 3) < GW;
+        float clip_hi = head_col ? p.logit_clip : -INFINITY;
+        float clip_lo = head_col ? -p.logit_clip : -INFINITY;
         bool first = true;
 
         // Clamp screen of key n of a tile (this lane: one group's codes): mean and E[x^2]
@@ -494,11 +496,11 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 #pragma unroll
                 for (int h = 0; h < GW; ++h) patch_val[wave][n][h] = part[h];
             }
-            if (n < GW) {
+            if (head_col) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int t = 4 * g + r;
-                    if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n] - m_run;
+                    if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n & 3] - m_run;
                 }
             }
         };
@@ -509,10 +511,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             if (nvalid < kTile) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    if (4 * g + r >= nvalid) {
-#pragma unroll
-                        for (int i = 0; i < NG / 2; ++i) f.vs[r * (NG / 2) + i] = 0u;
-                    }
+                    if (4 * g + r >= nvalid) f.vs[r] = (_Float16)0.0f;
                 }
             }
         };
@@ -574,13 +573,10 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             for (int i = 1; i < 8; ++i) smax = fmaxf(smax, s[i]);
             if (first || __builtin_amdgcn_ballot_w64(smax > 8.0f) != 0) {
                 const float mt = max_rows(smax);
-                // columns without a head (all -inf) contribute no move; the four group
-                // columns of a head (lanes n, n+4, n+8, n+12: each subtracts a quarter of
-                // its own m_run in qk) all take the head's move
+                // columns without a head (all -inf) do not move; the four columns of a head
+                // (each subtracts a quarter of its own m_run in qk) take the same move
                 const bool need = first ? mt > -INFINITY : mt > 8.0f;
-                float dm = need ? mt : 0.0f;
-                dm += row_dpp<kRowRor8>(dm);
-                dm += row_dpp<kRowRor4>(dm);
+                const float dm = need ? mt : 0.0f;
                 const float fct = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
                 m_run += dm;
                 clip_lo -= dm;
@@ -609,18 +605,16 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             clear_masked_scales(fa, nva);
             clear_masked_scales(fb, nvb);
 
+            // P' = p * scale rounded once to fp16 (v_fma_mix, relative error <= 2^-12): the
+            // output error stays below 2.4e-4 * max|v|.  Column n carries the V scales of
+            // group (n/4) % G, so one B operand serves every group: output column 4q + h is
+            // head h's for the d-tiles of group q, the other columns are not read.
+            h8_t pq;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pq[i] = (_Float16)__builtin_fmaf(pr[i], (float)(i < 4 ? fa.vs[i] : fb.vs[i - 4]), 0.0f);
             // ---- O^T += V^T P'^T over 32 tokens, one V scale group (two d-tiles) at a time ----
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
-                // P' = p * scale rounded once to fp16 (v_fma_mix, relative error <= 2^-12):
-                // the output error stays below 2.4e-4 * max|v|
-                h8_t pq;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int k = (i & 3) * NG + q;
-                    const h2_t v2 = __builtin_bit_cast(h2_t, i < 4 ? fa.vs[k >> 1] : fb.vs[k >> 1]);
-                    pq[i] = (_Float16)__builtin_fmaf(pr[i], (float)v2[k & 1], 0.0f);
-                }
                 uint32_t ka[4], kb[4];
                 biased_codes_to_f16(fa.v[q], ka);
                 biased_codes_to_f16(fb.v[q], kb);
@@ -677,19 +671,22 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         }
         __syncthreads();
 
-        // ---- wave result: column n < GW holds head n; lane (g, n) has d = 16j + 4g + r ----
+        // ---- wave result: column 4q + h holds head h for the d-tiles 2q, 2q + 1 of V scale
+        // group q; lane (g, n) has d = 16j + 4g + r ----
         l_run = add_rows(l_run);
-        if (n < GW) {
+        if (head_col) {
 #pragma unroll
             for (int j = 0; j < NDT; ++j) {
+                if ((n >> 2) == j / 2) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) comb[wave][n][2 + 16 * j + 4 * g + r] = acc[j][r];
+                    for (int r = 0; r < 4; ++r) comb[wave][n & 3][2 + 16 * j + 4 * g + r] = acc[j][r];
+                }
             }
-            if (g == 0) {
-                // a wave that scored no token: exp2 of its state's max is 0 in the merge
-                comb[wave][n][0] = first ? -1e30f : m_run;
-                comb[wave][n][1] = l_run;
-            }
+        }
+        if (n < GW && g == 0) {
+            // a wave that scored no token: exp2 of its state's max is 0 in the merge
+            comb[wave][n][0] = first ? -1e30f : m_run;
+            comb[wave][n][1] = l_run;
         }
         __syncthreads();
         finish_segment<D, GW>(p, comb, b, hq0, U, tile_begin, tile_end, pos == ws.lo ? 0 : 1);
