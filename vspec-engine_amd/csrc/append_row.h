@@ -60,6 +60,96 @@ __device__ __forceinline__ void apply_flag(const FlagOp& f) {
     else atomicAnd(f.word, ~f.bit);
 }
 
+// int4 codec of one 32-element group: rep = 2nd-largest |x|, scale = rep/8 (1 if rep == 0),
+// floored at 1e-6, rounded to fp16 (saturating), codes rint(x/scale) in [-8,7]; element e
+// in nibble e%8 of w[e/8].  c1, c2, cm: sum, sum of squares and largest magnitude of the
+// codes.
+struct Int4Group {
+    uint32_t w[4];
+    uint32_t s16;
+    float sc;
+    int c1, c2, cm;
+};
+// the largest two |x| seen (a1 >= a2; equal values count twice), updated with a
+__device__ __forceinline__ void int4_top2(float a, float& a1, float& a2) {
+    const bool gt1 = a > a1;
+    a2 = gt1 ? a1 : (a > a2 ? a : a2);
+    a1 = gt1 ? a : a1;
+}
+// fp16 bits of a group's scale from its 2nd-largest |x|
+__device__ __forceinline__ uint32_t int4_scale_bits(float rep) {
+    float scale = rep > 0.f ? rep / 8.0f : 1.0f;
+    if (scale < 1e-6f) scale = 1e-6f;
+    uint32_t s16 = float_to_half_bits(scale);
+    if ((s16 & 0x7fffu) >= 0x7c00u) s16 = 0x7bffu;
+    return s16;
+}
+__device__ __forceinline__ int int4_code(float x, float sc) {
+    const float rr = rintf(x / sc);
+    return rr > 7.0f ? 7 : (rr >= -8.0f ? (int)rr : -8);
+}
+__device__ __forceinline__ Int4Group int4_encode_group(const float (&x)[32]) {
+    float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) int4_top2(fabsf(x[e]), a1, a2);
+    Int4Group q;
+    q.s16 = int4_scale_bits(a2);
+    q.sc = half_bits_to_float(q.s16);
+    q.w[0] = q.w[1] = q.w[2] = q.w[3] = 0u;
+    q.c1 = q.c2 = q.cm = 0;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+        const int code = int4_code(x[e], q.sc);
+        q.w[e / 8] |= ((uint32_t)code & 0xfu) << (4 * (e % 8));
+        q.c1 += code;
+        q.c2 += code * code;
+        q.cm = max(q.cm, code < 0 ? -code : code);
+    }
+    return q;
+}
+
+// The clamp flag of a key from its row's sums: s1 = sum x, s2 = sum x^2 (the groups' scaled
+// code sums, added pairwise (g0 + g1) + (g2 + g3)) and m = max |x|.
+__device__ __forceinline__ bool int4_flag_from_sums(float s1, float s2, float m, uint32_t head_dim) {
+    const float mean = s1 / (float)head_dim;
+    const float ex2 = s2 / (float)head_dim;
+    const float var1 = ex2 - mean * mean;
+    const float th1 = fminf(fmaxf(1e-6f, 4.5f * sqrtf(fmaxf(var1, 0.f))), 16.0f);
+    return m > th1 * (1.0f - 0.0009765625f) || var1 <= ex2 * 0.0009765625f;
+}
+
+// Clamp flag of a key (attention_ref.c:56 clips every key at its std threshold): set when
+// some element may reach alpha * std (alpha 4.5, the reference default; threshold capped at
+// 16 as in 3-bit mode) of the dequantised row.  Mean and E[x^2] come from the code sums of
+// the row's groups, which sit in lanes 2c of an aligned run of 2 * head_dim / 32 lanes (the
+// append work items of one row: all of these lanes call this together); the 2^-10 margins
+// cover the one-pass variance (the decode kernel's screen test, run once per key here).
+__device__ __forceinline__ bool int4_key_flag(const Int4Group& q, uint32_t head_dim) {
+    float s1 = q.sc * (float)q.c1;
+    float s2 = (q.sc * q.sc) * (float)q.c2;
+    float m = q.sc * (float)q.cm;
+    for (uint32_t o = 2; o < 2 * (head_dim / 32); o <<= 1) {
+        s1 += __shfl_xor(s1, (int)o);
+        s2 += __shfl_xor(s2, (int)o);
+        m = fmaxf(m, __shfl_xor(m, (int)o));
+    }
+    return int4_flag_from_sums(s1, s2, m, head_dim);
+}
+
+// V code byte nn (0..15) of group c: d = 32c + nn in the low nibble, d = 32c + 16 + nn in
+// the high one (int4_v_byte places it).
+__device__ __forceinline__ uint32_t int4_v_group_byte(const uint32_t (&w)[4], int nn) {
+    const uint32_t lo = (w[nn / 8] >> (4 * (nn % 8))) & 0xfu;
+    const uint32_t hi = (w[2 + nn / 8] >> (4 * (nn % 8))) & 0xfu;
+    return lo | (hi << 4);
+}
+
+// Offset of V code byte nn of group c of token `slot` within its 16-token tile.
+__device__ __forceinline__ uint32_t int4_v_tile_byte(uint32_t slot, uint32_t c, uint32_t nn, uint32_t D) {
+    const uint32_t tt = slot & 15u, tg = tt >> 2, tr = tt & 3u;
+    return (16u * tg + nn) * (D / 8u) + 4u * c + 2u * (tr & 1u) + (tr >> 1);
+}
+
 template <int DT, int SRC>
 __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq, uint32_t pos, uint32_t h,
                                              uint32_t c, int which, size_t src_el, FlagOp* defer = nullptr) {
@@ -150,56 +240,9 @@ __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq
                            hb[6] | (hb[7] << 16));
         }
     } else {
-        // int4 codec: rep = 2nd-largest |x|, scale = rep/8 (1 if rep == 0),
-        // floored at 1e-6, rounded to fp16 (saturating), codes rint(x/scale) in [-8,7]
-        float a1 = 0.f, a2 = 0.f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float a = fabsf(x[e]);
-            if (a > a1) {
-                a2 = a1;
-                a1 = a;
-            } else if (a > a2) {
-                a2 = a;
-            }
-        }
-        float scale = a2 > 0.f ? a2 / 8.0f : 1.0f;
-        if (scale < 1e-6f) scale = 1e-6f;
-        uint32_t s16 = float_to_half_bits(scale);
-        if ((s16 & 0x7fffu) >= 0x7c00u) s16 = 0x7bffu;
-        const float sc = half_bits_to_float(s16);
-        uint32_t w[4] = {0u, 0u, 0u, 0u};
-        int c1 = 0, c2 = 0, cm = 0;  // sum, sum of squares and largest magnitude of the codes
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float rr = rintf(x[e] / sc);
-            const int code = rr > 7.0f ? 7 : (rr >= -8.0f ? (int)rr : -8);
-            w[e / 8] |= ((uint32_t)code & 0xfu) << (4 * (e % 8));
-            c1 += code;
-            c2 += code * code;
-            cm = max(cm, code < 0 ? -code : code);
-        }
+        const Int4Group q = int4_encode_group(x);
         if (!which && p.kf) {
-            // Clamp flag of the key (attention_ref.c:56 clips every key at its std threshold):
-            // set when some element may reach alpha * std (alpha 4.5, the reference default;
-            // threshold capped at 16 as in 3-bit mode) of the dequantised row.  Mean and
-            // E[x^2] come from the code sums of the row's groups, which sit in lanes 2c of
-            // an aligned run of 2 * head_dim / 32 lanes (the append work items of one row);
-            // the 2^-10 margins cover the one-pass variance (the decode kernel's screen test,
-            // run once per key here).
-            float s1 = sc * (float)c1;
-            float s2 = (sc * sc) * (float)c2;
-            float m = sc * (float)cm;
-            for (uint32_t o = 2; o < 2 * (p.head_dim / 32); o <<= 1) {
-                s1 += __shfl_xor(s1, (int)o);
-                s2 += __shfl_xor(s2, (int)o);
-                m = fmaxf(m, __shfl_xor(m, (int)o));
-            }
-            const float mean = s1 / (float)p.head_dim;
-            const float ex2 = s2 / (float)p.head_dim;
-            const float var1 = ex2 - mean * mean;
-            const float th1 = fminf(fmaxf(1e-6f, 4.5f * sqrtf(fmaxf(var1, 0.f))), 16.0f);
-            const bool flag = m > th1 * (1.0f - 0.0009765625f) || var1 <= ex2 * 0.0009765625f;
+            const bool flag = int4_key_flag(q, p.head_dim);
             if (c == 0) {
                 const FlagOp op = {p.kf + ((size_t)phys * p.hkv + h) * (p.block_tokens / 16) + slot / 16,
                                    1u << (slot % 16), flag};
@@ -211,23 +254,47 @@ __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq
         if (which) {
             // V tiles: byte n of this group's 16 holds d = 32c + n (low nibble) and
             // d = 32c + 16 + n (high nibble) of this token, at lane chunk (g, n)
-            const uint32_t tt = slot & 15u, tg = tt >> 2, tr = tt & 3u;
-            uint8_t* vb = dst + bh * ((size_t)p.block_tokens * p.head_dim / 2) +
-                          (size_t)(slot >> 4) * (8u * p.head_dim) + (size_t)(16u * tg) * (p.head_dim / 8u) +
-                          4u * c + 2u * (tr & 1u) + (tr >> 1);
+            uint8_t* vb = dst + bh * ((size_t)p.block_tokens * p.head_dim / 2) + (size_t)(slot >> 4) * (8u * p.head_dim);
 #pragma unroll
-            for (int nn = 0; nn < 16; ++nn) {
-                const uint32_t lo = (w[nn / 8] >> (4 * (nn % 8))) & 0xfu;
-                const uint32_t hi = (w[2 + nn / 8] >> (4 * (nn % 8))) & 0xfu;
-                vb[(size_t)nn * (p.head_dim / 8u)] = (uint8_t)(lo | (hi << 4));
-            }
-            p.vs[row * (p.head_dim / 32) + c] = (uint16_t)s16;
+            for (int nn = 0; nn < 16; ++nn) vb[int4_v_tile_byte(slot, c, nn, p.head_dim)] = (uint8_t)int4_v_group_byte(q.w, nn);
+            p.vs[row * (p.head_dim / 32) + c] = (uint16_t)q.s16;
         } else {
             uint4* d4 = reinterpret_cast<uint4*>(dst + row * (p.head_dim / 2) + e0 / 2);
-            *d4 = make_uint4(w[0], w[1], w[2], w[3]);
-            p.ks[int4_ks_index(bh, p.head_dim / 32, p.block_tokens, slot, c)] = (uint16_t)s16;
+            *d4 = make_uint4(q.w[0], q.w[1], q.w[2], q.w[3]);
+            p.ks[int4_ks_index(bh, p.head_dim / 32, p.block_tokens, slot, c)] = (uint16_t)q.s16;
         }
     }
+}
+
+// The append of a decode kernel's fused decode step: each sequence's new token at position
+// ctx_lens[b] - 1.
+__device__ __forceinline__ AppendParams decode_step_append_params(const DecodeParams& p, uint32_t head_dim) {
+    AppendParams a;
+    a.k = const_cast<uint8_t*>(p.k);
+    a.v = const_cast<uint8_t*>(p.v);
+    a.ks = const_cast<uint16_t*>(p.ks);
+    a.vs = const_cast<uint16_t*>(p.vs);
+    a.kf = const_cast<uint32_t*>(p.kf);
+    a.block_tables = p.block_tables;
+    a.start_pos = nullptr;
+    a.token_item = nullptr;
+    a.token_pos = nullptr;
+    a.n_items = 0;
+    a.rope_cos = nullptr;
+    a.rope_sin = nullptr;
+    a.rope_dim = 0;
+    a.max_pos = 0;
+    a.ctx_lens = p.ctx_lens;
+    a.k_new = p.k_new;
+    a.v_new = p.v_new;
+    a.batch = p.batch;
+    a.n_new = 1;
+    a.hkv = p.hkv;
+    a.head_dim = head_dim;
+    a.block_tokens = p.block_tokens;
+    a.max_blocks = p.max_blocks;
+    a.num_blocks = p.num_blocks;
+    return a;
 }
 
 // Work items of one append launch: 2 (K, V) x chunks per row x kv heads x tokens.
@@ -286,30 +353,7 @@ __device__ void fused_append(const DecodeParams& p, const WorkSplit& ws, ItemCur
     constexpr int EPT = append_ept(DT);
     constexpr int kItems = D / EPT * 2;  // append work items per token-head row (K and V)
     static_assert(kItems <= kWaves * 64, "one pass of the workgroup's threads");
-    AppendParams a;
-    a.k = const_cast<uint8_t*>(p.k);
-    a.v = const_cast<uint8_t*>(p.v);
-    a.ks = const_cast<uint16_t*>(p.ks);
-    a.vs = const_cast<uint16_t*>(p.vs);
-    a.kf = const_cast<uint32_t*>(p.kf);
-    a.block_tables = p.block_tables;
-    a.start_pos = nullptr;
-    a.token_item = nullptr;
-    a.token_pos = nullptr;
-    a.rope_cos = nullptr;
-    a.rope_sin = nullptr;
-    a.rope_dim = 0;
-    a.max_pos = 0;
-    a.ctx_lens = p.ctx_lens;
-    a.k_new = p.k_new;
-    a.v_new = p.v_new;
-    a.batch = p.batch;
-    a.n_new = 1;
-    a.hkv = p.hkv;
-    a.head_dim = D;
-    a.block_tokens = p.block_tokens;
-    a.max_blocks = p.max_blocks;
-    a.num_blocks = p.num_blocks;
+    const AppendParams a = decode_step_append_params(p, D);
     const int t = (int)threadIdx.x;
     // int4 clamp flags (thread 0 of each row): the first one is handed back to the caller,
     // which applies it after the barrier below (so the barrier does not wait for it) and,

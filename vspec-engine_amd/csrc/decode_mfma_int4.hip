@@ -125,6 +125,18 @@ struct I4Stage {
 };
 constexpr int kLoadsPerPair = 8;  // LDS loads per tile pair (K, V, K scales, V scales per tile)
 
+// A decode step's new token as its pool writes will hold it: the K row's codes, the V code
+// bytes of each group c (byte n at 16c + n, as int4_v_tile_byte places them in the tile),
+// the K and V scales and the key's clamp flag.
+template <int D>
+struct I4NewToken {
+    uint4 k[D / 32];
+    uint32_t vb[D / 8];
+    uint16_t ks[D / 32];
+    uint16_t vs[D / 32];
+    uint32_t flag;
+};
+
 #ifndef VSPEC_I4_MIN_WG_PER_CU
 #define VSPEC_I4_MIN_WG_PER_CU 2
 #endif
@@ -157,13 +169,6 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 
     const int ips = (int)(p.hkv * p.gsplit);  // work items per sequence
     const WorkSplit ws = work_split<kSplitAlways>(p, ips, split_sh);
-    FlagOp pending = {nullptr, 0u, false};
-    __shared__ uint32_t pend_lds[3];  // the fused append's first clamp flag: {word, bit, value}
-    if (FL && threadIdx.x == 0) pend_lds[0] = 0xffffffffu;
-    // Set-up of the range's first work item overlaps the fused append: its q rows are
-    // loaded before the append, and its first tile pairs are on their way before the
-    // barrier that publishes the append (pairs that may hold the appended token wait
-    // behind that barrier).  The threads that stored wait for their stores first.
     // q rows of a work item (wave w < GW: head w), loaded ahead of the item's set-up
     constexpr int E = D / 64;
     float q_rows[E];
@@ -175,17 +180,131 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             for (int e = 0; e < E; ++e) q_rows[e] = qrow[lane * E + e];
         }
     };
+    ItemCursor c0 = {0, 0, 1, 0, 0};
     if (ws.lo < ws.hi) {
-        const ItemCursor c0 = cursor_at(p, ws);
+        c0 = cursor_at(p, ws);
         load_q(c0.b, c0.y);
     }
     const bool appending = p.k_new != nullptr && ws.lo < ws.hi;
-    if (appending) {
-        fused_append<VSPEC_KV_INT4, D, false>(p, ws, cursor_at(p, ws), ips, pending, FL ? pend_lds : nullptr);
-        __builtin_amdgcn_s_waitcnt(0);  // this thread's stores (and q loads) are done
+    // The fused decode step's new token of the range's first work item, when the range holds
+    // that item's last tile (exactly one workgroup appends each item) and the token's
+    // position lies in the table.  Lanes below kNtLanes of wave 0 (4 elements of the K or
+    // V row each) quantise it from the source rows alone into `nt` before the workgroup's
+    // first barrier; the tile loop copies it into the stage of the item's last tile once
+    // that tile has landed, and its clamp flag into the tile's flag word, so the launch never
+    // waits for its own pool writes, which lanes below kAppendLanes (one group of K, even
+    // lanes, or V, odd lanes) issue after the item's tile loop.
+    constexpr int kNtLanes = 16 * NG;
+    constexpr int kAppendLanes = 2 * NG;
+    static_assert(kNtLanes <= 64, "the new token's lanes fit one wave");
+    __shared__ I4NewToken<D> nt;
+    const int ctx0 = appending ? as_const(p.ctx_lens)[c0.b] : 0;
+    const bool nt_in = appending && c0.item0 + c0.U <= ws.hi && ctx0 > 0 &&
+                       ctx0 <= (int)(p.max_blocks * p.block_tokens);
+    const uint32_t nt_pos = nt_in ? (uint32_t)ctx0 - 1u : 0u;
+    const uint32_t nt_slot = nt_pos % kTile;  // in its tile
+    const uint32_t nt_bit = 1u << nt_slot;
+    int nt_phys = -1;  // (appending lanes) table entry of the token's block
+    if (appending && wave == 0) {
+        if (nt_in && lane < kNtLanes) {
+            // lane (row, c, k): elements 4k..4k+3 of group c of the K (row 0) or V row; the
+            // group's 2nd-largest |x|, code sums and V bytes come from its 8 lanes, so every
+            // value equals the one-lane encoding of the append kernel (int4_encode_group)
+            const int row = lane / (8 * NG), c = (lane >> 3) % NG, k = lane & 7;
+            const size_t src_el = ((size_t)c0.b * p.hkv + (uint32_t)c0.y / p.gsplit) * D + 32 * c + 4 * k;
+            const uint8_t* src = row ? p.v_new : p.k_new;
+            float x[4];
+            if (p.append_src == VSPEC_KV_F32) {
+                const float4 w = *reinterpret_cast<const float4*>(src + src_el * 4);
+                x[0] = w.x; x[1] = w.y; x[2] = w.z; x[3] = w.w;
+            } else {
+                const uint2 w = *reinterpret_cast<const uint2*>(src + src_el * 2);
+                x[0] = half_bits_to_float(w.x & 0xffffu); x[1] = half_bits_to_float(w.x >> 16);
+                x[2] = half_bits_to_float(w.y & 0xffffu); x[3] = half_bits_to_float(w.y >> 16);
+            }
+            // a vector load (the barriers wait for scalar ones), used after the tile loop
+            const __amdgpu_buffer_rsrc_t trow = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<int32_t*>(p.block_tables + (size_t)c0.b * p.max_blocks), (short)0,
+                (int)(4u * p.max_blocks), 0x00020000);
+            nt_phys = __builtin_amdgcn_raw_buffer_load_b32(trow, (int)(4u * (nt_pos / p.block_tokens)), 0, 0);
+            // the top two |x| of the lane, merged over the group (exact: comparisons only)
+            float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) int4_top2(fabsf(x[e]), a1, a2);
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) {
+                const float b1 = __shfl_xor(a1, o), b2 = __shfl_xor(a2, o);
+                a2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
+                a1 = fmaxf(a1, b1);
+            }
+            const uint32_t s16 = int4_scale_bits(a2);
+            const float sc = half_bits_to_float(s16);
+            uint32_t chunk = 0u;  // the 4 codes, element 4k + e in nibble e
+            int c1 = 0, c2 = 0, cm = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int code = int4_code(x[e], sc);
+                chunk |= ((uint32_t)code & 0xfu) << (4 * e);
+                c1 += code;
+                c2 += code * code;
+                cm = max(cm, code < 0 ? -code : code);
+            }
+            if (row == 0) {
+                // K: codes at bytes 16c + 2k of the row; the key's clamp flag from the row's
+                // sums, the groups added pairwise as int4_key_flag adds them
+#pragma unroll
+                for (int o = 1; o < 8; o <<= 1) {
+                    c1 += __shfl_xor(c1, o);
+                    c2 += __shfl_xor(c2, o);
+                    cm = max(cm, __shfl_xor(cm, o));
+                }
+                float s1 = sc * (float)c1, s2 = (sc * sc) * (float)c2, m = sc * (float)cm;
+#pragma unroll
+                for (int o = 8; o < 8 * NG; o <<= 1) {
+                    s1 += __shfl_xor(s1, o);
+                    s2 += __shfl_xor(s2, o);
+                    m = fmaxf(m, __shfl_xor(m, o));
+                }
+                reinterpret_cast<uint16_t*>(nt.k)[8 * c + k] = (uint16_t)chunk;
+                if (k == 0) nt.ks[c] = (uint16_t)s16;
+                if (lane == 0) nt.flag = p.kf && int4_flag_from_sums(s1, s2, m, D) ? 1u : 0u;
+            } else {
+                // V: byte n of group c holds d = 32c + n (low nibble, lane n/4) and d = 32c + 16 + n
+                // (high nibble, lane 4 + n/4)
+                const uint32_t hi = (uint32_t)__shfl(chunk, lane + 4);
+                if (k < 4) {
+                    uint32_t w4 = 0u;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w4 |= (((chunk >> (4 * e)) & 0xfu) | (((hi >> (4 * e)) & 0xfu) << 4)) << (8 * e);
+                    nt.vb[4 * c + k] = w4;
+                }
+                if (k == 0) nt.vs[c] = (uint16_t)s16;
+            }
+        }
+        // The range's further appended items (short ones) are written to the pool at once,
+        // and their tiles are read after the first barrier: these lanes wait for their stores.
+        ItemCursor c = c0;
+        bool direct = false;
+        while (c.item0 + c.U < ws.hi) {
+            cursor_next(p, ips, c);
+            const int ctx = as_const(p.ctx_lens)[c.b];
+            if (c.item0 + c.U <= ws.hi && ctx > 0) {
+                direct = true;
+                if (lane < kAppendLanes) {
+                    const AppendParams a = decode_step_append_params(p, D);
+                    const size_t src_el = ((size_t)c.b * p.hkv + (uint32_t)c.y / p.gsplit) * D + (size_t)(lane >> 1) * 32;
+                    if (p.append_src == VSPEC_KV_F32) {
+                        append_chunk<VSPEC_KV_INT4, VSPEC_KV_F32>(a, (uint32_t)c.b, (uint32_t)ctx - 1u,
+                                                                  (uint32_t)c.y / p.gsplit, (uint32_t)lane >> 1, lane & 1, src_el);
+                    } else {
+                        append_chunk<VSPEC_KV_INT4, VSPEC_KV_F16>(a, (uint32_t)c.b, (uint32_t)ctx - 1u,
+                                                                  (uint32_t)c.y / p.gsplit, (uint32_t)lane >> 1, lane & 1, src_el);
+                    }
+                }
+            }
+        }
+        if (direct) __builtin_amdgcn_s_waitcnt(0);
     }
-    uint32_t pend_word = 0xffffffffu, pend_bit = 0u, pend_val = 0u;
-    bool first_item = true;
     int b = ws.b;
     int seq0 = ws.seq0;
     for (int pos = ws.lo; pos < ws.hi;) {
@@ -300,6 +419,21 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 #pragma unroll
             for (int r = 0; r < 4; ++r) f.vs[r] = vs[r * NG];
         };
+        // nt over whatever the load of its tile (stage tile h, landed) read at its slot:
+        // the K row's 16-byte chunks where the K load put them, the K scales (group-major
+        // rows of 16) and V scales (token-major) of the slot, and the V code bytes
+        auto patch_new_token = [&](I4Stage& st, const int h) {
+            if (lane < D / 32) st.k[h][NQ == 4 ? 16 * lane + (int)nt_slot : 2 * (int)nt_slot + lane] = nt.k[lane];
+            uint16_t* sc16 = reinterpret_cast<uint16_t*>(&st.sc[h][0]);
+            if (lane < NG) {
+                sc16[16 * lane + nt_slot] = nt.ks[lane];
+                sc16[64 + NG * nt_slot + lane] = nt.vs[lane];
+            }
+            if (lane < 16 * NG) {
+                reinterpret_cast<uint8_t*>(&st.v[h][0])[int4_v_tile_byte(nt_slot, (uint32_t)lane >> 4, (uint32_t)lane & 15u, D)] =
+                    reinterpret_cast<const uint8_t*>(nt.vb)[lane];
+            }
+        };
 
         const int step = 2 * kWaves;
         const int t0 = tile_begin + 2 * wave;
@@ -326,36 +460,19 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             for (int e = 0; e < E; ++e) qs[wave][lane * E + e] = fminf(fmaxf(x[e], -th), th) * p.qscale;
         }
         // The first ST pairs are on their way while the q operands are prepared (after the
-        // q rows are in registers: a wait for those would also wait for these).  In the
-        // range's first item, pairs of any wave that may reach the appended token's tile
-        // (the item's last, when this workgroup appended it) are issued after the barrier.
-        const bool defer = first_item && appending && tile_end == U &&
-                           tile_begin + 2 * (kWaves - 1) + (ST - 1) * step + 1 >= U - 1;
+        // q rows are in registers: a wait for those would also wait for these).
         // the ring's first table reads go out together
         Look first_look[ST];
 #pragma unroll
         for (int u = 0; u < ST; ++u) first_look[u] = lookup(t0 + u * step);
-        if (!defer) {
 #pragma unroll
-            for (int u = 0; u < ST; ++u) issue(t0 + u * step, u, first_look[u]);
-        }
+        for (int u = 0; u < ST; ++u) issue(t0 + u * step, u, first_look[u]);
         Look next = lookup(t0 + ST * step);
         __syncthreads();
-        if (first_item) {
-            if (FL) {
-                pend_word = __builtin_amdgcn_readfirstlane(pend_lds[0]);
-                pend_bit = __builtin_amdgcn_readfirstlane(pend_lds[1]);
-                pend_val = __builtin_amdgcn_readfirstlane(pend_lds[2]);
-            }
-            // the append's first flag update, after the barrier (a tile read of its word
-            // takes the patched value)
-            apply_flag(pending);
-            if (defer) {
-#pragma unroll
-                for (int u = 0; u < ST; ++u) issue(t0 + u * step, u, first_look[u]);
-            }
-            first_item = false;
-        }
+        // this item takes its new token from nt (written before the barrier): the token's
+        // slot in the item's last tile, and its clamp flag bit in that tile's flag word
+        const bool nt_item = nt_in && pos == ws.lo;
+        const uint32_t nt_val = nt_item && __builtin_amdgcn_readfirstlane(nt.flag) ? nt_bit : 0u;
 
         // ---- QK B operands: k-slots 8g..8g+7 of MFMA m carry code dword dw = g*NQ + m in
         // the order e = 0,4,1,5,2,6,3,7; column n takes group n/4 of head n%4 ----
@@ -523,13 +640,15 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                           float (&pr)[8]) {
             // clamp flags: from the pool, or from the screen (both tiles in one basic block:
             // their chains interleave)
-            // the tile this launch appended into: its word with the appended key's flag
-            // patched in, or (another appended item of this range) the screen
-            const bool scr_a = !flags_on || (fused && tile_a == U - 1 && fa.fword != pend_word);
-            const bool scr_b = !flags_on || (fused && tile_a + 1 == U - 1 && fb.fword != pend_word);
-            auto word_of = [&](const I4Frags<D>& f) -> uint32_t {
+            // the tile this launch appended into: its word with nt's flag bit in (the item
+            // that takes nt), or (another appended item of this range) the screen
+            const bool nt_a = nt_item && tile_a == U - 1;
+            const bool nt_b = nt_item && tile_a + 1 == U - 1;
+            const bool scr_a = !flags_on || (fused && tile_a == U - 1 && !nt_item);
+            const bool scr_b = !flags_on || (fused && tile_a + 1 == U - 1 && !nt_item);
+            auto word_of = [&](const I4Frags<D>& f, const bool nt_t) -> uint32_t {
                 const uint32_t w = __builtin_amdgcn_readfirstlane(f.flags);
-                return f.fword == pend_word ? (w & ~pend_bit) | pend_val : w;
+                return nt_t ? (w & ~nt_bit) | nt_val : w;
             };
             uint32_t fla, flb;
             f4_t sa, sb;
@@ -538,13 +657,13 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 const Screen snb = screen(fb, nvb);
                 sa = qk(fa);
                 sb = qk(fb);
-                fla = scr_a ? tokens(__builtin_amdgcn_ballot_w64(sna.flag)) : word_of(fa) & valid_mask(nva);
-                flb = scr_b ? tokens(__builtin_amdgcn_ballot_w64(snb.flag)) : word_of(fb) & valid_mask(nvb);
+                fla = scr_a ? tokens(__builtin_amdgcn_ballot_w64(sna.flag)) : word_of(fa, nt_a) & valid_mask(nva);
+                flb = scr_b ? tokens(__builtin_amdgcn_ballot_w64(snb.flag)) : word_of(fb, nt_b) & valid_mask(nvb);
             } else {
                 sa = qk(fa);
                 sb = qk(fb);
-                fla = word_of(fa) & valid_mask(nva);
-                flb = word_of(fb) & valid_mask(nvb);
+                fla = word_of(fa, nt_a) & valid_mask(nva);
+                flb = word_of(fb, nt_b) & valid_mask(nvb);
             }
             if ((fla | flb) != 0u) {
                 if (fla != 0u) exact(fa, fla, sa);
@@ -644,6 +763,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 const int nvb = max(0, min(capb, ctx - (t + 1) * kTile));
                 const bool live = capa > 0 || capb > 0;
                 float pr[8];
+                if (nt_item && (t == U - 1 || t + 1 == U - 1)) patch_new_token(stg[u][wave], t == U - 1 ? 0 : 1);
                 if (live) {
                     fetch_k(stg[u][wave], 0, fa);
                     fetch_k(stg[u][wave], 1, fb);
@@ -661,6 +781,27 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // every load has landed before the ring is reused (the wave results below share
         // its memory) or the wave ends
         wait_loads<0>();
+        // nt into the pool (and its flag into the pool's flag word), after the item's tiles:
+        // nothing in this launch reads it back
+        if (nt_item && wave == 0 && lane < kAppendLanes && nt_phys >= 0 && (uint32_t)nt_phys < p.num_blocks) {
+            const uint32_t slot = nt_pos % (uint32_t)P;
+            const size_t bh = (size_t)nt_phys * p.hkv + hk;
+            const int ch = lane >> 1;
+            if (!(lane & 1)) {
+                *reinterpret_cast<uint4*>(const_cast<uint8_t*>(p.k) + (bh * P + slot) * (D / 2) + 16 * ch) = nt.k[ch];
+                const_cast<uint16_t*>(p.ks)[int4_ks_index(bh, NG, P, slot, ch)] = nt.ks[ch];
+                if (ch == 0 && p.kf) {
+                    apply_flag({const_cast<uint32_t*>(p.kf) + bh * (P / kTile) + slot / kTile, 1u << (slot % kTile),
+                                nt.flag != 0u});
+                }
+            } else {
+                uint8_t* vt = const_cast<uint8_t*>(p.v) + bh * ((size_t)P * D / 2) + (size_t)(slot / kTile) * (8 * D);
+                const uint8_t* vb = reinterpret_cast<const uint8_t*>(nt.vb) + 16 * ch;
+#pragma unroll
+                for (int nn = 0; nn < 16; ++nn) vt[int4_v_tile_byte(slot, ch, nn, D)] = vb[nn];
+                const_cast<uint16_t*>(p.vs)[(bh * P + slot) * NG + ch] = nt.vs[ch];
+            }
+        }
         // the next item's q rows load while this one's states are merged
         if (item0 + tile_end < ws.hi) {
             const int npos = item0 + tile_end;
