@@ -227,16 +227,18 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 const_cast<int32_t*>(p.block_tables + (size_t)c0.b * p.max_blocks), (short)0,
                 (int)(4u * p.max_blocks), 0x00020000);
             nt_phys = __builtin_amdgcn_raw_buffer_load_b32(trow, (int)(4u * (nt_pos / p.block_tokens)), 0, 0);
-            // the top two |x| of the lane, merged over the group (exact: comparisons only)
+            // the top two |x| of the lane, merged over the group's lanes by DPP moves (its
+            // quad partners, then the other quad: exact, comparisons only)
             float a1 = 0.f, a2 = 0.f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) int4_top2(fabsf(x[e]), a1, a2);
-#pragma unroll
-            for (int o = 1; o < 8; o <<= 1) {
-                const float b1 = __shfl_xor(a1, o), b2 = __shfl_xor(a2, o);
+            auto merge_top2 = [&](const float b1, const float b2) {
                 a2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
                 a1 = fmaxf(a1, b1);
-            }
+            };
+            merge_top2(dpp<kQuadXor1>(a1), dpp<kQuadXor1>(a2));
+            merge_top2(dpp<kQuadXor2>(a1), dpp<kQuadXor2>(a2));
+            merge_top2(dpp<kRowHalfMirror>(a1), dpp<kRowHalfMirror>(a2));
             const uint32_t s16 = int4_scale_bits(a2);
             const float sc = half_bits_to_float(s16);
             uint32_t chunk = 0u;  // the 4 codes, element 4k + e in nibble e
@@ -252,18 +254,21 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             if (row == 0) {
                 // K: codes at bytes 16c + 2k of the row; the key's clamp flag from the row's
                 // sums, the groups added pairwise as int4_key_flag adds them
-#pragma unroll
-                for (int o = 1; o < 8; o <<= 1) {
-                    c1 += __shfl_xor(c1, o);
-                    c2 += __shfl_xor(c2, o);
-                    cm = max(cm, __shfl_xor(cm, o));
-                }
-                float s1 = sc * (float)c1, s2 = (sc * sc) * (float)c2, m = sc * (float)cm;
-#pragma unroll
-                for (int o = 8; o < 8 * NG; o <<= 1) {
-                    s1 += __shfl_xor(s1, o);
-                    s2 += __shfl_xor(s2, o);
-                    m = fmaxf(m, __shfl_xor(m, o));
+                // (integer code sums: exact in fp32 in any order)
+                const float gc1 = group_sum<8>((float)c1), gc2 = group_sum<8>((float)c2);
+                float gcm = (float)cm;
+                gcm = fmaxf(gcm, dpp<kQuadXor1>(gcm));
+                gcm = fmaxf(gcm, dpp<kQuadXor2>(gcm));
+                gcm = fmaxf(gcm, dpp<kRowHalfMirror>(gcm));
+                float s1 = sc * gc1, s2 = (sc * sc) * gc2, m = sc * gcm;
+                // group g0 + g1 (lane ^ 8: the row's other half), then (g0 + g1) + (g2 + g3)
+                s1 += row_dpp<kRowRor8>(s1);
+                s2 += row_dpp<kRowRor8>(s2);
+                m = fmaxf(m, row_dpp<kRowRor8>(m));
+                if constexpr (NG == 4) {
+                    s1 = add_xor16(s1);
+                    s2 = add_xor16(s2);
+                    m = max_xor16(m);
                 }
                 reinterpret_cast<uint16_t*>(nt.k)[8 * c + k] = (uint16_t)chunk;
                 if (k == 0) nt.ks[c] = (uint16_t)s16;
@@ -271,7 +276,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             } else {
                 // V: byte n of group c holds d = 32c + n (low nibble, lane n/4) and d = 32c + 16 + n
                 // (high nibble, lane 4 + n/4)
-                const uint32_t hi = (uint32_t)__shfl(chunk, lane + 4);
+                const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)chunk, kRowRor12, 0xf, 0xf, true);  // lane + 4
                 if (k < 4) {
                     uint32_t w4 = 0u;
 #pragma unroll
@@ -447,14 +452,12 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 x[e] = q_rows[e];
                 s += x[e];
             }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+            s = wave_sum(s);
             const float mean = s * (1.0f / D);
             float v = 0.f;
 #pragma unroll
             for (int e = 0; e < E; ++e) v = fmaf(x[e] - mean, x[e] - mean, v);
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+            v = wave_sum(v);
             const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v * (1.0f / D))), p.input_clip);
 #pragma unroll
             for (int e = 0; e < E; ++e) qs[wave][lane * E + e] = fminf(fmaxf(x[e], -th), th) * p.qscale;

@@ -65,8 +65,10 @@ constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
 constexpr int kRowHalfMirror = 0x141;
 constexpr int kRowMirror = 0x140;
-constexpr int kRowRor4 = 0x124;     // rotate by 4 lanes inside each row of 16
+// rotations inside each row of 16: lane i takes lane i - n (mod 16) of its row
+constexpr int kRowRor4 = 0x124;
 constexpr int kRowRor8 = 0x128;
+constexpr int kRowRor12 = 0x12C;    // lane i takes lane i + 4 of its row
 
 // x(lane) combined with x(lane ^ 16) / x(lane ^ 32) through the gfx950 permlane swaps
 // (VALU, no LDS).  v_permlane16_swap exchanges the odd 16-lane rows of its first
