@@ -52,20 +52,20 @@ def gpu():
     return torch.device("cuda:0")
 
 
-@pytest.fixture(params=["plan", "always"])
+@pytest.fixture(params=["plan", "always", "never"])
 def flag_gate(request):
-    """int4 decode: "plan" lets the host pick the clamp-flag kernel (shares of >= 64 tiles
+    """int4 decode: "plan" lets the host pick the clamp-flag kernel (shares of >= 16 tiles
     per workgroup) or the screen-every-tile one; "always" forces the flag kernel
-    (VSPEC_ROCM_DECODE_FLAG_MIN_TILES=0, read on every call).  Cases of other pool
-    dtypes run once."""
+    (VSPEC_ROCM_DECODE_FLAG_MIN_TILES=0, read on every call), "never" the screen one
+    (4096).  Cases of other pool dtypes run once."""
     import os
 
     dtype = request.node.callspec.params.get("dtype", DTYPE_INT4)
-    if request.param == "always" and dtype != DTYPE_INT4:
+    if request.param != "plan" and dtype != DTYPE_INT4:
         pytest.skip("clamp flags exist for int4 pools only")
     old = os.environ.get("VSPEC_ROCM_DECODE_FLAG_MIN_TILES")
-    if request.param == "always":
-        os.environ["VSPEC_ROCM_DECODE_FLAG_MIN_TILES"] = "0"
+    if request.param != "plan":
+        os.environ["VSPEC_ROCM_DECODE_FLAG_MIN_TILES"] = "0" if request.param == "always" else "4096"
     yield request.param
     if old is None:
         os.environ.pop("VSPEC_ROCM_DECODE_FLAG_MIN_TILES", None)

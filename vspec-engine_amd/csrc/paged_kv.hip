@@ -821,8 +821,10 @@ uint32_t decode_segment_cost() {
 
 // int4 clamp flags are read by the decode only when the balanced split gives each workgroup
 // at least this many tiles (VSPEC_ROCM_DECODE_FLAG_MIN_TILES, 0..4096); shorter shares read
-// no flags and screen every tile.  Read on every call.
-constexpr uint32_t kDefaultFlagMinTiles = 64;
+// no flags and screen every tile.  Measured (fused step, µs): C3 (32 tiles per workgroup)
+// 23.1 with flags against 23.9 screening; B = 8 at 4k 23.2 against 24.0; B = 1-4 equal;
+// B = 16 at 6k 38.6 against 40.7.  Read on every call.
+constexpr uint32_t kDefaultFlagMinTiles = 16;
 uint32_t decode_flag_min_tiles() {
     const char* e = getenv("VSPEC_ROCM_DECODE_FLAG_MIN_TILES");
     const long x = e ? strtol(e, nullptr, 10) : -1;
