@@ -45,6 +45,7 @@ WORKLOADS = {
     "qwen3-8b-b16-ctx2k-int4": dict(B=16, T=2049, Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
     "qwen3-8b-b64-ctx4k-int4": dict(B=64, T=4097, Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
     "qwen3-8b-b64-ctx128-8k": dict(B=64, ctx_range=(128, 8192), Hq=32, Hkv=8, D=128, P=16, dtype="f16"),
+    "qwen3-8b-b64-ctx128-8k-int4": dict(B=64, ctx_range=(128, 8192), Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
     "qwen3-8b-b8-chunk512-evict-int4": dict(B=8, flow="c5", Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
 }
 

@@ -727,14 +727,34 @@ def test_decode_step_fused_append(oracle, gpu, flag_gate, dtype, Hq, Hkv, D, P, 
     the oracle's append (bit-exact) and attention (within tolerance).  Contexts include 0
     (nothing appended) and 1 (the new token alone); GQA group 8 makes two q-head groups
     share each kv head's last tile; P=32 puts two tiles in a block."""
+    say(f"[decode-step] dtype={dtype} Hq={Hq} Hkv={Hkv} D={D} P={P} pt={pt} src16={src16}")
+    ctx = np.array([1, 17, 40, 0, 100, 33, 16], np.int32)
+    _fused_step_case(oracle, gpu, dtype, Hq, Hkv, D, P, pt, src16, ctx, seed=71 + D + P + dtype)
+
+
+@pytest.mark.parametrize("dtype,D", [(DTYPE_INT4, 128), (DTYPE_INT4, 64), (DTYPE_F16, 128)])
+@pytest.mark.parametrize("pt", [64, 256, 0])
+def test_decode_step_many_short_items(oracle, gpu, flag_gate, dtype, D, pt):
+    """The fused decode step where one workgroup's range ends many work items: 48 sequences
+    of 0-48 tokens over ranges of 4 or 16 tiles (partition_tokens 64 / 256) or the balanced
+    split, so that each range appends several tokens (in the int4 kernel the range's first
+    item through its LDS record, the others written to the pool by all waves before the
+    first barrier).  Pool bytes, clamp flags and outputs equal the separate append + decode
+    flow, and the oracle."""
+    say(f"[decode-step short items] dtype={dtype} D={D} pt={pt}")
+    rng = np.random.default_rng(5150 + D + pt)
+    ctx = rng.integers(0, 49, 48).astype(np.int32)
+    ctx[:3] = [0, 1, 16]
+    _fused_step_case(oracle, gpu, dtype, 32, 8, D, 16, pt, True, ctx, seed=91 + D + pt + dtype)
+
+
+def _fused_step_case(oracle, gpu, dtype, Hq, Hkv, D, P, pt, src16, ctx, seed):
     import copy
 
     import torch
     import vspec_rocm as vr
 
-    say(f"[decode-step] dtype={dtype} Hq={Hq} Hkv={Hkv} D={D} P={P} pt={pt} src16={src16}")
-    ctx = np.array([1, 17, 40, 0, 100, 33, 16], np.int32)
-    full = make_case(oracle, dtype, len(ctx), Hq, Hkv, D, P, ctx, seed=71 + D + P + dtype, src16=src16)
+    full = make_case(oracle, dtype, len(ctx), Hq, Hkv, D, P, ctx, seed=seed, src16=src16)
     pre = [copy.copy(full) for _ in range(2)]
     pools = []
     for c in pre:

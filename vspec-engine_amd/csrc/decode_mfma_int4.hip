@@ -205,105 +205,139 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
     const uint32_t nt_slot = nt_pos % kTile;  // in its tile
     const uint32_t nt_bit = 1u << nt_slot;
     int nt_phys = -1;  // (appending lanes) table entry of the token's block
-    if (appending && wave == 0) {
-        if (nt_in && lane < kNtLanes) {
-            // lane (row, c, k): elements 4k..4k+3 of group c of the K (row 0) or V row; the
-            // group's 2nd-largest |x|, code sums and V bytes come from its 8 lanes, so every
-            // value equals the one-lane encoding of the append kernel (int4_encode_group)
-            const int row = lane / (8 * NG), c = (lane >> 3) % NG, k = lane & 7;
-            const size_t src_el = ((size_t)c0.b * p.hkv + (uint32_t)c0.y / p.gsplit) * D + 32 * c + 4 * k;
-            const uint8_t* src = row ? p.v_new : p.k_new;
-            float x[4];
-            if (p.append_src == VSPEC_KV_F32) {
-                const float4 w = *reinterpret_cast<const float4*>(src + src_el * 4);
-                x[0] = w.x; x[1] = w.y; x[2] = w.z; x[3] = w.w;
-            } else {
-                const uint2 w = *reinterpret_cast<const uint2*>(src + src_el * 2);
-                x[0] = half_bits_to_float(w.x & 0xffffu); x[1] = half_bits_to_float(w.x >> 16);
-                x[2] = half_bits_to_float(w.y & 0xffffu); x[3] = half_bits_to_float(w.y >> 16);
-            }
-            // a vector load (the barriers wait for scalar ones), used after the tile loop
-            const __amdgpu_buffer_rsrc_t trow = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<int32_t*>(p.block_tables + (size_t)c0.b * p.max_blocks), (short)0,
-                (int)(4u * p.max_blocks), 0x00020000);
-            nt_phys = __builtin_amdgcn_raw_buffer_load_b32(trow, (int)(4u * (nt_pos / p.block_tokens)), 0, 0);
-            // the top two |x| of the lane, merged over the group's lanes by DPP moves (its
-            // quad partners, then the other quad: exact, comparisons only)
-            float a1 = 0.f, a2 = 0.f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) int4_top2(fabsf(x[e]), a1, a2);
-            auto merge_top2 = [&](const float b1, const float b2) {
-                a2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
-                a1 = fmaxf(a1, b1);
-            };
-            merge_top2(dpp<kQuadXor1>(a1), dpp<kQuadXor1>(a2));
-            merge_top2(dpp<kQuadXor2>(a1), dpp<kQuadXor2>(a2));
-            merge_top2(dpp<kRowHalfMirror>(a1), dpp<kRowHalfMirror>(a2));
-            const uint32_t s16 = int4_scale_bits(a2);
-            const float sc = half_bits_to_float(s16);
-            uint32_t chunk = 0u;  // the 4 codes, element 4k + e in nibble e
-            int c1 = 0, c2 = 0, cm = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int code = int4_code(x[e], sc);
-                chunk |= ((uint32_t)code & 0xfu) << (4 * e);
-                c1 += code;
-                c2 += code * code;
-                cm = max(cm, code < 0 ? -code : code);
-            }
-            if (row == 0) {
-                // K: codes at bytes 16c + 2k of the row; the key's clamp flag from the row's
-                // sums, the groups added pairwise as int4_key_flag adds them
-                // (integer code sums: exact in fp32 in any order)
-                const float gc1 = group_sum<8>((float)c1), gc2 = group_sum<8>((float)c2);
-                float gcm = (float)cm;
-                gcm = fmaxf(gcm, dpp<kQuadXor1>(gcm));
-                gcm = fmaxf(gcm, dpp<kQuadXor2>(gcm));
-                gcm = fmaxf(gcm, dpp<kRowHalfMirror>(gcm));
-                float s1 = sc * gc1, s2 = (sc * sc) * gc2, m = sc * gcm;
-                // group g0 + g1 (lane ^ 8: the row's other half), then (g0 + g1) + (g2 + g3)
-                s1 += row_dpp<kRowRor8>(s1);
-                s2 += row_dpp<kRowRor8>(s2);
-                m = fmaxf(m, row_dpp<kRowRor8>(m));
-                if constexpr (NG == 4) {
-                    s1 = add_xor16(s1);
-                    s2 = add_xor16(s2);
-                    m = max_xor16(m);
-                }
-                reinterpret_cast<uint16_t*>(nt.k)[8 * c + k] = (uint16_t)chunk;
-                if (k == 0) nt.ks[c] = (uint16_t)s16;
-                if (lane == 0) nt.flag = p.kf && int4_flag_from_sums(s1, s2, m, D) ? 1u : 0u;
-            } else {
-                // V: byte n of group c holds d = 32c + n (low nibble, lane n/4) and d = 32c + 16 + n
-                // (high nibble, lane 4 + n/4)
-                const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)chunk, kRowRor12, 0xf, 0xf, true);  // lane + 4
-                if (k < 4) {
-                    uint32_t w4 = 0u;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) w4 |= (((chunk >> (4 * e)) & 0xfu) | (((hi >> (4 * e)) & 0xfu) << 4)) << (8 * e);
-                    nt.vb[4 * c + k] = w4;
-                }
-                if (k == 0) nt.vs[c] = (uint16_t)s16;
-            }
+    // Lane (row, c, k) of a token's encoding holds elements 4k..4k+3 of group c of the K
+    // (row 0) or V row (lanes below kNtLanes).
+    const int e_row = lane / (8 * NG), e_c = (lane >> 3) % NG, e_k = lane & 7;
+    auto load_token = [&](const int bb, const uint32_t hk, float (&x)[4]) {
+        const size_t src_el = ((size_t)bb * p.hkv + hk) * D + 32 * e_c + 4 * e_k;
+        const uint8_t* src = e_row ? p.v_new : p.k_new;
+        if (p.append_src == VSPEC_KV_F32) {
+            const float4 w = *reinterpret_cast<const float4*>(src + src_el * 4);
+            x[0] = w.x; x[1] = w.y; x[2] = w.z; x[3] = w.w;
+        } else {
+            const uint2 w = *reinterpret_cast<const uint2*>(src + src_el * 2);
+            x[0] = half_bits_to_float(w.x & 0xffffu); x[1] = half_bits_to_float(w.x >> 16);
+            x[2] = half_bits_to_float(w.y & 0xffffu); x[3] = half_bits_to_float(w.y >> 16);
         }
-        // The range's further appended items (short ones) are written to the pool at once,
-        // and their tiles are read after the first barrier: these lanes wait for their stores.
+    };
+    // One token quantised by the lanes below kNtLanes of a wave: the group's 2nd-largest |x|,
+    // code sums and V bytes come from its 8 lanes, so every value equals the one-lane encoding
+    // of the append kernel (int4_encode_group).  The lane's 4 codes (element 4k + e in nibble
+    // e, at bytes 16c + 2k of a K row), for V lanes with k < 4 the V code bytes n = 4k..4k+3
+    // of group c, the group's scale bits and (lane 0) the key's clamp flag.
+    struct TokenLane {
+        uint32_t chunk, vword, s16;
+        bool flag;
+    };
+    auto encode_token = [&](const float (&x)[4]) -> TokenLane {
+        TokenLane r = {0u, 0u, 0u, false};
+        // the top two |x| of the lane, merged over the group's lanes by DPP moves (its
+        // quad partners, then the other quad: exact, comparisons only)
+        float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) int4_top2(fabsf(x[e]), a1, a2);
+        auto merge_top2 = [&](const float b1, const float b2) {
+            a2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
+            a1 = fmaxf(a1, b1);
+        };
+        merge_top2(dpp<kQuadXor1>(a1), dpp<kQuadXor1>(a2));
+        merge_top2(dpp<kQuadXor2>(a1), dpp<kQuadXor2>(a2));
+        merge_top2(dpp<kRowHalfMirror>(a1), dpp<kRowHalfMirror>(a2));
+        r.s16 = int4_scale_bits(a2);
+        const float sc = half_bits_to_float(r.s16);
+        int c1 = 0, c2 = 0, cm = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int code = int4_code(x[e], sc);
+            r.chunk |= ((uint32_t)code & 0xfu) << (4 * e);
+            c1 += code;
+            c2 += code * code;
+            cm = max(cm, code < 0 ? -code : code);
+        }
+        if (e_row == 0) {
+            // the key's clamp flag from the row's sums, the groups added pairwise as
+            // int4_key_flag adds them (integer code sums: exact in fp32 in any order)
+            const float gc1 = group_sum<8>((float)c1), gc2 = group_sum<8>((float)c2);
+            float gcm = (float)cm;
+            gcm = fmaxf(gcm, dpp<kQuadXor1>(gcm));
+            gcm = fmaxf(gcm, dpp<kQuadXor2>(gcm));
+            gcm = fmaxf(gcm, dpp<kRowHalfMirror>(gcm));
+            float s1 = sc * gc1, s2 = (sc * sc) * gc2, m = sc * gcm;
+            // group g0 + g1 (lane ^ 8: the row's other half), then (g0 + g1) + (g2 + g3)
+            s1 += row_dpp<kRowRor8>(s1);
+            s2 += row_dpp<kRowRor8>(s2);
+            m = fmaxf(m, row_dpp<kRowRor8>(m));
+            if constexpr (NG == 4) {
+                s1 = add_xor16(s1);
+                s2 = add_xor16(s2);
+                m = max_xor16(m);
+            }
+            r.flag = p.kf && int4_flag_from_sums(s1, s2, m, D);
+        } else {
+            // V: byte n of group c holds d = 32c + n (low nibble, lane n/4) and d = 32c + 16 + n
+            // (high nibble, lane 4 + n/4)
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)r.chunk, kRowRor12, 0xf, 0xf, true);  // lane + 4
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r.vword |= (((r.chunk >> (4 * e)) & 0xfu) | (((hi >> (4 * e)) & 0xfu) << 4)) << (8 * e);
+        }
+        return r;
+    };
+    if (appending && wave == 0 && nt_in && lane < kNtLanes) {
+        float x[4];
+        load_token(c0.b, (uint32_t)c0.y / p.gsplit, x);
+        // a vector load (the barriers wait for scalar ones), used after the tile loop
+        const __amdgpu_buffer_rsrc_t trow = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(p.block_tables + (size_t)c0.b * p.max_blocks), (short)0,
+            (int)(4u * p.max_blocks), 0x00020000);
+        nt_phys = __builtin_amdgcn_raw_buffer_load_b32(trow, (int)(4u * (nt_pos / p.block_tokens)), 0, 0);
+        const TokenLane tl = encode_token(x);
+        if (e_row == 0) {
+            reinterpret_cast<uint16_t*>(nt.k)[8 * e_c + e_k] = (uint16_t)tl.chunk;
+            if (e_k == 0) nt.ks[e_c] = (uint16_t)tl.s16;
+            if (lane == 0) nt.flag = tl.flag ? 1u : 0u;
+        } else {
+            if (e_k < 4) nt.vb[4 * e_c + e_k] = tl.vword;
+            if (e_k == 0) nt.vs[e_c] = (uint16_t)tl.s16;
+        }
+    }
+    // The range's further appended items (short ones), the j-th of them by wave j % kWaves,
+    // are written to the pool at once (the same bytes as the append kernel's), and their
+    // tiles are read after the first barrier: these waves wait for their stores.
+    if (appending) {
+        const uint32_t P0 = PB ? (uint32_t)PB : p.block_tokens;
         ItemCursor c = c0;
         bool direct = false;
+        int j = 0;
         while (c.item0 + c.U < ws.hi) {
             cursor_next(p, ips, c);
             const int ctx = as_const(p.ctx_lens)[c.b];
-            if (c.item0 + c.U <= ws.hi && ctx > 0) {
-                direct = true;
-                if (lane < kAppendLanes) {
-                    const AppendParams a = decode_step_append_params(p, D);
-                    const size_t src_el = ((size_t)c.b * p.hkv + (uint32_t)c.y / p.gsplit) * D + (size_t)(lane >> 1) * 32;
-                    if (p.append_src == VSPEC_KV_F32) {
-                        append_chunk<VSPEC_KV_INT4, VSPEC_KV_F32>(a, (uint32_t)c.b, (uint32_t)ctx - 1u,
-                                                                  (uint32_t)c.y / p.gsplit, (uint32_t)lane >> 1, lane & 1, src_el);
-                    } else {
-                        append_chunk<VSPEC_KV_INT4, VSPEC_KV_F16>(a, (uint32_t)c.b, (uint32_t)ctx - 1u,
-                                                                  (uint32_t)c.y / p.gsplit, (uint32_t)lane >> 1, lane & 1, src_el);
+            if (c.item0 + c.U > ws.hi || ctx <= 0) continue;
+            if (j++ % kWaves != wave || ctx > (int)(p.max_blocks * P0)) continue;
+            direct = true;
+            const uint32_t pos = (uint32_t)ctx - 1u, hk = (uint32_t)c.y / p.gsplit;
+            const int phys = as_const(p.block_tables)[(size_t)c.b * p.max_blocks + pos / P0];
+            if (lane < kNtLanes) {
+                float x[4];
+                load_token(c.b, hk, x);
+                const TokenLane tl = encode_token(x);
+                if (phys >= 0 && (uint32_t)phys < p.num_blocks) {
+                    const uint32_t slot = pos % P0;
+                    const size_t bh = (size_t)phys * p.hkv + hk;
+                    if (e_row == 0) {
+                        *reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(p.k) + (bh * P0 + slot) * (D / 2) + 16 * e_c + 2 * e_k) =
+                            (uint16_t)tl.chunk;
+                        if (e_k == 0) const_cast<uint16_t*>(p.ks)[int4_ks_index(bh, NG, P0, slot, e_c)] = (uint16_t)tl.s16;
+                        if (lane == 0 && p.kf) {
+                            apply_flag({const_cast<uint32_t*>(p.kf) + bh * (P0 / kTile) + slot / kTile,
+                                        1u << (slot % kTile), tl.flag});
+                        }
+                    } else if (e_k < 4) {
+                        uint8_t* vt = const_cast<uint8_t*>(p.v) + bh * ((size_t)P0 * D / 2) + (size_t)(slot / kTile) * (8 * D);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            vt[int4_v_tile_byte(slot, e_c, 4 * e_k + e, D)] = (uint8_t)(tl.vword >> (8 * e));
+                        }
+                        if (e_k == 0) const_cast<uint16_t*>(p.vs)[(bh * P0 + slot) * NG + e_c] = (uint16_t)tl.s16;
                     }
                 }
             }
