@@ -991,10 +991,11 @@ def test_decode_wide_whole_items(oracle, gpu, D, Hq, Hkv, P, B, T, monkeypatch):
     check_attention(oracle, case, got.cpu().numpy(), 1)
 
 
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_INT4])
 @pytest.mark.parametrize("seg_cost", [0, 3, 16, 64])
-def test_decode_ragged_segment_cost(oracle, gpu, seg_cost, monkeypatch):
-    """Ragged f16 batches split over a cost axis on which every work item also costs
-    seg_cost tiles (VSPEC_ROCM_DECODE_SEGMENT_COST): workgroup ranges start and end inside
+def test_decode_ragged_segment_cost(oracle, gpu, seg_cost, dtype, monkeypatch):
+    """Ragged batches split over a cost axis on which every work item also costs seg_cost
+    tiles (VSPEC_ROCM_DECODE_SEGMENT_COST, ..._INT4): workgroup ranges start and end inside
     items' set-up units and inside their tiles, some are empty, items meet many workgroups
     or none.  Many short sequences beside long ones, GQA 4 and 8 (two q-head groups per kv
     head), plain decode and fused decode step: every output against the oracle, the step's
@@ -1005,14 +1006,14 @@ def test_decode_ragged_segment_cost(oracle, gpu, seg_cost, monkeypatch):
     import torch
     import vspec_rocm as vr
 
-    monkeypatch.setenv("VSPEC_ROCM_DECODE_SEGMENT_COST", str(seg_cost))
-    say(f"[segment cost] cost={seg_cost}")
+    monkeypatch.setenv("VSPEC_ROCM_DECODE_SEGMENT_COST" + ("_INT4" if dtype == DTYPE_INT4 else ""), str(seg_cost))
+    say(f"[segment cost] dtype={dtype} cost={seg_cost}")
     ctx = np.array([1, 17, 3000, 16, 33, 5, 200, 64, 2, 1500, 48, 129, 7, 4100, 31, 90] * 2, np.int32)
     for Hq in (32, 64):
-        case = make_case(oracle, DTYPE_F16, len(ctx), Hq, 8, 128, 16, ctx, seed=900 + seg_cost + Hq)
+        case = make_case(oracle, dtype, len(ctx), Hq, 8, 128, 16, ctx, seed=900 + seg_cost + Hq + dtype)
         pre = copy.copy(case)
         pre.ctx = (case.ctx - 1).astype(np.int32)
-        pre.host = HostPool(DTYPE_F16, case.num_blocks, 16, 8, 128)
+        pre.host = HostPool(dtype, case.num_blocks, 16, 8, 128)
         fill_garbage(pre.host)
         pool = build_both(oracle, pre, gpu)
         B = len(ctx)

@@ -464,7 +464,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
             if (lane >= o) x += y;
         }
         int umin = b < nb ? u : 0x7fffffff, umax = u;
-        if constexpr (UNEVEN == kSplitRagged) {
+        if constexpr (UNEVEN != 0) {
 #pragma unroll
             for (int o = 32; o; o >>= 1) {
                 umin = min(umin, __shfl_xor(umin, o));
@@ -484,13 +484,13 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         for (int w = 0; w < NW; ++w) {
             before += w < wave ? sh.wsum[w] : 0;
             all += sh.wsum[w];
-            if constexpr (UNEVEN == kSplitRagged) {
+            if constexpr (UNEVEN != 0) {
                 umin = min(umin, sh.umin[w]);
                 umax = max(umax, sh.umax[w]);
             }
         }
         r.tiles = __builtin_amdgcn_readfirstlane(all) * ips;
-        r.ragged = UNEVEN == kSplitRagged ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
+        r.ragged = UNEVEN != 0 ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
         r.alpha = split_alpha(p, r.ragged);
         r.total = r.tiles + r.alpha * ips * nb;
         split_range<UNEVEN>(p, r);
@@ -530,7 +530,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
     for (int b = threadIdx.x; b < nb; b += NW * 64) {
         const int u = item_tiles(p, b);
         s += u;
-        if constexpr (UNEVEN == kSplitRagged) {
+        if constexpr (UNEVEN != 0) {
             umin = min(umin, u);
             umax = max(umax, u);
         }
@@ -538,7 +538,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
 #pragma unroll
     for (int o = 32; o; o >>= 1) {
         s += __shfl_xor(s, o);
-        if constexpr (UNEVEN == kSplitRagged) {
+        if constexpr (UNEVEN != 0) {
             umin = min(umin, __shfl_xor(umin, o));
             umax = max(umax, __shfl_xor(umax, o));
         }
@@ -559,7 +559,7 @@ __device__ __forceinline__ WorkSplit work_split(const DecodeParams& p, int ips, 
         umax = max(umax, sh.umax[w]);
     }
     r.tiles = __builtin_amdgcn_readfirstlane(units) * ips;
-    r.ragged = UNEVEN == kSplitRagged ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
+    r.ragged = UNEVEN != 0 ? __builtin_amdgcn_readfirstlane(umin != umax ? 1 : 0) : 0;
     r.alpha = split_alpha(p, r.ragged);
     r.total = r.tiles + r.alpha * ips * nb;
     split_range<UNEVEN>(p, r);
@@ -785,7 +785,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_merge_split(DecodeParams p
             umax = max(umax, sh.umax[v]);
         }
         w.tiles = all * ips;
-        w.ragged = UNEVEN == kSplitRagged && umin != umax ? 1 : 0;
+        w.ragged = UNEVEN != 0 && umin != umax ? 1 : 0;
         w.alpha = split_alpha(p, w.ragged);
         w.total = w.tiles + w.alpha * ips * nb;
     }

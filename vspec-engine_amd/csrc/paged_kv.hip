@@ -820,6 +820,19 @@ uint32_t decode_segment_cost() {
     return x >= 0 && x <= 64 ? (uint32_t)x : kDefaultSegmentCost;
 }
 
+// The same for int4 pools (VSPEC_ROCM_DECODE_SEGMENT_COST_INT4, 0..64), whose work items
+// cost more set-up against their tiles (q operands, three barriers, the merge of the waves'
+// states): decode step at the C4 shape with int4 KV (64 sequences, contexts U[128, 8192])
+// with a cost of 0 / 8 / 16 / 24 / 32 / 40 / 48 / 64 tiles: 128.8 / 105.4 / 86.7 / 81.4 /
+// 79.2 / 78.6 / 78.0 / 81.6 us; two other seeds 124.6 -> 86.3 (40) and 104.7 -> 86.8 (32,
+// 48); C5 decode 53.8 -> 50.8 (32) / 51.2 (48).  Read on every call.
+constexpr uint32_t kDefaultSegmentCostInt4 = 40;
+uint32_t decode_segment_cost_int4() {
+    const char* e = getenv("VSPEC_ROCM_DECODE_SEGMENT_COST_INT4");
+    const long x = e ? strtol(e, nullptr, 10) : -1;
+    return x >= 0 && x <= 64 ? (uint32_t)x : kDefaultSegmentCostInt4;
+}
+
 // int4 clamp flags are read by the decode only when the balanced split gives each workgroup
 // at least this many tiles (VSPEC_ROCM_DECODE_FLAG_MIN_TILES, 0..4096); shorter shares read
 // no flags and screen every tile.  Measured (fused step, µs): C3 (32 tiles per workgroup)
@@ -955,10 +968,16 @@ int plan_decode(const VspecPagedAttnDesc* d, DecodePlan* pl) {
             uint32_t wpc = decode_wgs_per_cu_env();
             if (!wpc) wpc = d->kv.dtype == VSPEC_KV_F16 && bound < 128ull * (uint64_t)num_cus() ? 1u : 2u;
             grid = (uint64_t)wpc * (uint64_t)num_cus();
-            // the kernel caps its groups at total / min_tiles of the actual tiles; the grid
-            // (from the bound, which is at least the total) only trims idle workgroups
+            // the kernel caps its groups at total / min_tiles of the actual split total (tiles,
+            // plus the segment cost of every work item of a ragged batch); the grid, from a
+            // bound of that total, only trims idle workgroups, so the split does not depend on
+            // the host's context bound
+            const uint64_t seg = d->kv.dtype == VSPEC_KV_F16    ? decode_segment_cost()
+                                 : d->kv.dtype == VSPEC_KV_INT4 ? decode_segment_cost_int4()
+                                                                : 0u;
+            const uint64_t cost_bound = bound + seg * (uint64_t)d->batch * hkv * pl->gsplit;
             const uint64_t min_tiles = pl->min_tiles;
-            if (grid * min_tiles > bound) grid = bound / min_tiles;
+            if (grid * min_tiles > cost_bound) grid = cost_bound / min_tiles;
         }
         pl->grid_x = (uint32_t)(grid ? grid : 1);
         pl->split_tiles = bound;
@@ -1479,7 +1498,9 @@ int paged_decode(const VspecPagedAttnDesc* desc, const void* k_new, const void* 
     p.uniform_tiles = pl.split ? pl.uniform_tiles : 0u;
     p.min_tiles = pl.split && !pl.chunk_tiles ? pl.min_tiles : 1u;
     p.wide = pl.wide;
-    p.seg_cost = desc->kv.dtype == VSPEC_KV_F16 && pl.split && !pl.chunk_tiles ? decode_segment_cost() : 0u;
+    p.seg_cost = !pl.split || pl.chunk_tiles ? 0u
+                 : desc->kv.dtype == VSPEC_KV_F16 ? decode_segment_cost()
+                 : desc->kv.dtype == VSPEC_KV_INT4 ? decode_segment_cost_int4() : 0u;
 
     hipStream_t s = (hipStream_t)desc->stream;
     if (k_new) {
