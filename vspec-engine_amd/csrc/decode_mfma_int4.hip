@@ -414,7 +414,8 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             tile = __builtin_amdgcn_readfirstlane(tile);
             const bool ok = tile < tile_end && entry >= 0 && (uint32_t)entry < p.num_blocks;
             const int slot0 = (tile % tiles_per_block) * kTile;
-            const size_t bh = (size_t)(ok ? entry : 0) * p.hkv + hk;
+            // block x head index in 32 bits (check_kv bounds num_blocks * hkv)
+            const size_t bh = (uint32_t)(ok ? entry : 0) * p.hkv + (uint32_t)hk;
             const uint32_t code_bytes = ok ? 8u * D : 0u;
             lds_load16(lds_addr(&st.k[h][0]), tile_rsrc(p.k + (bh * P + slot0) * (D / 2), code_bytes), off_k);
             lds_load16(lds_addr(&st.v[h][0]),
@@ -538,6 +539,14 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         }
         __syncthreads();
         const float kbias = kbias_lds[n];
+        // the B operands stay in registers for the whole item (32 VGPRs): read from LDS per
+        // pair they cost 8 reads and a wait before each score MFMA
+        h8_t qreg[NQ][2];
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) {
+            qreg[m][0] = __builtin_bit_cast(h8_t, qb_lds[m][0][lane]);
+            qreg[m][1] = __builtin_bit_cast(h8_t, qb_lds[m][1][lane]);
+        }
 
         f4_t acc[NDT];
 #pragma unroll
@@ -554,6 +563,8 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         float clip_hi = head_col ? p.logit_clip : -INFINITY;
         float clip_lo = head_col ? -p.logit_clip : -INFINITY;
         bool first = true;
+        // every column holds a head and the logits are not clipped: the clip is the identity
+        const bool clip_on = GW < 4 || p.logit_clip < INFINITY;
 
         // Clamp screen of key n of a tile (this lane: one group's codes): mean and E[x^2]
         // from integer code sums; this group's |x| <= 8 * scale.  `flag` is set in a lane
@@ -599,8 +610,8 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 uint32_t pr4[4];
                 k_codes_to_f16(f.k[m], pr4);
                 const h8_t a = __builtin_bit_cast(h8_t, make_uint4(pr4[0], pr4[1], pr4[2], pr4[3]));
-                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, qb_lds[m][0][lane]), sacc, 0, 0, 0);
-                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, qb_lds[m][1][lane]), sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qreg[m][0], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qreg[m][1], sacc, 0, 0, 0);
             }
             const h2_t kc[2] = {__builtin_bit_cast(h2_t, f.ks_col.x), __builtin_bit_cast(h2_t, f.ks_col.y)};
             const float mq = -0.25f * m_run;
@@ -714,8 +725,12 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             float s[8];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                s[r] = __builtin_amdgcn_fmed3f(sa[r], clip_lo, clip_hi);
-                s[4 + r] = __builtin_amdgcn_fmed3f(sb[r], clip_lo, clip_hi);
+                s[r] = sa[r];
+                s[4 + r] = sb[r];
+            }
+            if (clip_on) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s[i] = __builtin_amdgcn_fmed3f(s[i], clip_lo, clip_hi);
             }
             if (nva < kTile || nvb < kTile) {
 #pragma unroll

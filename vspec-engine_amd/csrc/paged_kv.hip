@@ -665,6 +665,11 @@ int check_kv(const VspecPagedKV* kv, const char* who, bool decode = false) {
         set_err("%s: empty pool geometry", who);
         return 0;
     }
+    // the kernels index (block, kv head) pairs in 32 bits
+    if ((uint64_t)kv->num_blocks * kv->num_kv_heads > 0xffffffffull) {
+        set_err("%s: num_blocks x num_kv_heads must fit 32 bits", who);
+        return 0;
+    }
     const uint32_t quantum = kv->dtype == VSPEC_KV_INT4 ? 32u : 8u;
     if (kv->head_dim % quantum != 0) {
         set_err("%s: head_dim must be a multiple of %u", who, quantum);
