@@ -85,6 +85,20 @@ def test_argument_validation_without_gpu():
     d.kv.num_kv_heads = 4
     assert L.vspec_rocm_paged_decode_workspace_bytes(C.byref(d)) == 0
     assert "multiple" in vspec_rocm.last_error()
+    # block indices are int32 table entries and (block, kv head) pairs are indexed in 32 bits
+    d.num_q_heads = 8
+    d.kv.num_blocks = 0x80000000
+    assert L.vspec_rocm_paged_decode_workspace_bytes(C.byref(d)) == 0
+    assert "num_blocks" in vspec_rocm.last_error()
+    d.kv.num_blocks = 0x40000000  # x 4 kv heads = 2^32
+    assert L.vspec_rocm_paged_decode_workspace_bytes(C.byref(d)) == 0
+    assert "num_blocks" in vspec_rocm.last_error()
+    # the int4 buffer descriptors hold address bits 0..47
+    d.kv.num_blocks = 4
+    d.kv.k_scales = d.kv.v_scales = 0x1000
+    d.kv.k_data = 1 << 47
+    assert L.vspec_rocm_paged_decode_workspace_bytes(C.byref(d)) == 0
+    assert "2^47" in vspec_rocm.last_error()
     be = L.vspec_make_rocm_backend()
     assert be.name == b"rocm-gfx950"
 

@@ -95,8 +95,9 @@ typedef int32_t rsrc_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(base);
-    // word 1: base bits 32..47, stride 0; word 3: 32-bit data format (raw buffer access)
-    return rsrc_t{(int32_t)(uint32_t)a, (int32_t)((uint32_t)(a >> 32) & 0xffffu), (int32_t)bytes, 0x00020000};
+    // word 1: base bits 32..47, stride 0 (the host admits pool addresses below 2^47, so
+    // bits 48..63 are zero); word 3: 32-bit data format (raw buffer access)
+    return rsrc_t{(int32_t)(uint32_t)a, (int32_t)(uint32_t)(a >> 32), (int32_t)bytes, 0x00020000};
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)reinterpret_cast<uintptr_t>(p); }
 // 16 (4) bytes per lane from the descriptor's base + voff into LDS at lds + 16 (4) * lane
@@ -372,7 +373,8 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // work item's last token
         const bool flags_on = FL && p.alpha >= 4.5f;
         const bool fused = p.k_new != nullptr;
-        auto valid_mask = [](int nvalid) -> uint32_t { return nvalid >= kTile ? 0xffffu : (1u << nvalid) - 1u; };
+        // nvalid is at most kTile (16): the shift stays below 32
+        auto valid_mask = [](int nvalid) -> uint32_t { return (1u << nvalid) - 1u; };
 
         // ---- tile pairs into this wave's LDS ring ----
         // Per-lane byte offsets of the loads: K lane (g, n) takes token n's code dwords
@@ -412,23 +414,26 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         auto issue_tile = [&](int tile, const int entry, const int used, I4Stage& st, const int h, int& cap,
                               uint32_t& flag, uint32_t& fword) {
             tile = __builtin_amdgcn_readfirstlane(tile);
-            const bool ok = tile < tile_end && entry >= 0 && (uint32_t)entry < p.num_blocks;
+            // 1 when the tile is in the range and its entry a valid block (the host bounds
+            // num_blocks by INT32_MAX, so a negative entry fails the unsigned compare); kept
+            // as an integer, which stays on the scalar unit without lane-mask conversions
+            const uint32_t ok = (uint32_t)(tile < tile_end) & (uint32_t)((uint32_t)entry < p.num_blocks);
             const int slot0 = (tile % tiles_per_block) * kTile;
             // block x head index in 32 bits (check_kv bounds num_blocks * hkv)
-            const size_t bh = (uint32_t)(ok ? entry : 0) * p.hkv + (uint32_t)hk;
-            const uint32_t code_bytes = ok ? 8u * D : 0u;
+            const size_t bh = ((uint32_t)entry & (0u - ok)) * p.hkv + (uint32_t)hk;
+            const uint32_t code_bytes = ok * (8u * D);
             lds_load16(lds_addr(&st.k[h][0]), tile_rsrc(p.k + (bh * P + slot0) * (D / 2), code_bytes), off_k);
             lds_load16(lds_addr(&st.v[h][0]),
                        tile_rsrc(p.v + bh * ((size_t)P * D / 2) + (size_t)(slot0 / kTile) * (8 * D), code_bytes), off_v);
             if (lane < 8 * NG) {
                 lds_load4(lds_addr(&st.sc[h][0]),
-                          tile_rsrc(p.ks + bh * NG * P + slot0, ok ? (uint32_t)(((NG - 1) * P + kTile) * 2) : 0u), off_ks);
-                lds_load4(lds_addr(&st.sc[h][32]), tile_rsrc(p.vs + (bh * P + slot0) * NG, ok ? 32u * NG : 0u), off_vs);
+                          tile_rsrc(p.ks + bh * NG * P + slot0, ok * (uint32_t)(((NG - 1) * P + kTile) * 2)), off_ks);
+                lds_load4(lds_addr(&st.sc[h][32]), tile_rsrc(p.vs + (bh * P + slot0) * NG, ok * (32u * NG)), off_vs);
             }
             fword = (uint32_t)(bh * (P / kTile) + slot0 / kTile);
             flag = flags_on ? (uint32_t)as_const(reinterpret_cast<const int32_t*>(p.kf))[fword] : 0u;
             if constexpr (USED) cap = ok ? used_cap(used, slot0) : 0;
-            else cap = ok ? kTile : 0;
+            else cap = (int)ok * kTile;
         };
         auto issue = [&](int tile_a, int u, const Look& l) {
             issue_tile(tile_a, l.entry[0], l.used[0], stg[u][wave], 0, cap_s[u][0], flag_s[u][0], fword_s[u][0]);
@@ -511,6 +516,8 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // slot in the item's last tile, and its clamp flag bit in that tile's flag word
         const bool nt_item = nt_in && pos == ws.lo;
         const uint32_t nt_val = nt_item && __builtin_amdgcn_readfirstlane(nt.flag) ? nt_bit : 0u;
+        // the tile this launch appended into without taking nt: its flags come from the screen
+        const int scr_tile = fused && !nt_item ? U - 1 : -2;
 
         // ---- QK B operands: k-slots 8g..8g+7 of MFMA m carry code dword dw = g*NQ + m in
         // the order e = 0,4,1,5,2,6,3,7; column n takes group n/4 of head n%4 ----
@@ -689,15 +696,11 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             // clamp flags: from the pool, or from the screen (both tiles in one basic block:
             // their chains interleave)
             // the tile this launch appended into: its word with nt's flag bit in (the item
-            // that takes nt), or (another appended item of this range) the screen
-            const bool nt_a = nt_item && tile_a == U - 1;
-            const bool nt_b = nt_item && tile_a + 1 == U - 1;
-            const bool scr_a = !flags_on || (fused && tile_a == U - 1 && !nt_item);
-            const bool scr_b = !flags_on || (fused && tile_a + 1 == U - 1 && !nt_item);
-            auto word_of = [&](const I4Frags<D>& f, const bool nt_t) -> uint32_t {
-                const uint32_t w = __builtin_amdgcn_readfirstlane(f.flags);
-                return nt_t ? (w & ~nt_bit) | nt_val : w;
-            };
+            // that takes nt: patched in the tile loop), or (another appended item of this
+            // range) the screen
+            const bool scr_a = !flags_on || tile_a == scr_tile;
+            const bool scr_b = !flags_on || tile_a + 1 == scr_tile;
+            auto word_of = [&](const I4Frags<D>& f) -> uint32_t { return __builtin_amdgcn_readfirstlane(f.flags); };
             uint32_t fla, flb;
             f4_t sa, sb;
             if (scr_a || scr_b) {
@@ -705,13 +708,13 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 const Screen snb = screen(fb, nvb);
                 sa = qk(fa);
                 sb = qk(fb);
-                fla = scr_a ? tokens(__builtin_amdgcn_ballot_w64(sna.flag)) : word_of(fa, nt_a) & valid_mask(nva);
-                flb = scr_b ? tokens(__builtin_amdgcn_ballot_w64(snb.flag)) : word_of(fb, nt_b) & valid_mask(nvb);
+                fla = scr_a ? tokens(__builtin_amdgcn_ballot_w64(sna.flag)) : word_of(fa) & valid_mask(nva);
+                flb = scr_b ? tokens(__builtin_amdgcn_ballot_w64(snb.flag)) : word_of(fb) & valid_mask(nvb);
             } else {
                 sa = qk(fa);
                 sb = qk(fb);
-                fla = word_of(fa, nt_a) & valid_mask(nva);
-                flb = word_of(fb, nt_b) & valid_mask(nvb);
+                fla = word_of(fa) & valid_mask(nva);
+                flb = word_of(fb) & valid_mask(nvb);
             }
             if ((fla | flb) != 0u) {
                 if (fla != 0u) exact(fa, fla, sa);
@@ -815,7 +818,12 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 const int nvb = max(0, min(capb, ctx - (t + 1) * kTile));
                 const bool live = capa > 0 || capb > 0;
                 float pr[8];
-                if (nt_item && (t == U - 1 || t + 1 == U - 1)) patch_new_token(stg[u][wave], t == U - 1 ? 0 : 1);
+                if (nt_item && (t == U - 1 || t + 1 == U - 1)) {
+                    patch_new_token(stg[u][wave], t == U - 1 ? 0 : 1);
+                    // nt's clamp flag bit in its tile's flag word
+                    if (t == U - 1) fa.flags = (fa.flags & ~nt_bit) | nt_val;
+                    else fb.flags = (fb.flags & ~nt_bit) | nt_val;
+                }
                 if (live) {
                     fetch_k(stg[u][wave], 0, fa);
                     fetch_k(stg[u][wave], 1, fb);

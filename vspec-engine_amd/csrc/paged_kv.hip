@@ -665,9 +665,9 @@ int check_kv(const VspecPagedKV* kv, const char* who, bool decode = false) {
         set_err("%s: empty pool geometry", who);
         return 0;
     }
-    // the kernels index (block, kv head) pairs in 32 bits
-    if ((uint64_t)kv->num_blocks * kv->num_kv_heads > 0xffffffffull) {
-        set_err("%s: num_blocks x num_kv_heads must fit 32 bits", who);
+    // block-table entries are int32, and the kernels index (block, kv head) pairs in 32 bits
+    if (kv->num_blocks > 0x7fffffffu || (uint64_t)kv->num_blocks * kv->num_kv_heads > 0xffffffffull) {
+        set_err("%s: num_blocks must fit int32 and num_blocks x num_kv_heads 32 bits", who);
         return 0;
     }
     const uint32_t quantum = kv->dtype == VSPEC_KV_INT4 ? 32u : 8u;
@@ -693,6 +693,14 @@ int check_kv(const VspecPagedKV* kv, const char* who, bool decode = false) {
     }
     if (kv->dtype == VSPEC_KV_INT4 && (!kv->k_scales || !kv->v_scales)) {
         set_err("%s: int4 pool without scales", who);
+        return 0;
+    }
+    // the int4 decode builds buffer descriptors whose base field holds address bits 0..47
+    // (device addresses of user allocations lie below 2^47)
+    const uintptr_t hi = ((uintptr_t)kv->k_data | (uintptr_t)kv->v_data | (uintptr_t)kv->k_scales |
+                          (uintptr_t)kv->v_scales | (uintptr_t)kv->k_flags) >> 47;
+    if (hi != 0) {
+        set_err("%s: pool address at or above 2^47", who);
         return 0;
     }
     return 1;
