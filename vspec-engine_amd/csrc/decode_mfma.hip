@@ -162,7 +162,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
     __shared__ float qraw[kQStage][GW][D];
     __shared__ float qs[NW][GW][D];  // per wave: q' of its current item
     // per wave: QK B operands (hi, lo for each 32-wide d chunk), read back every tile
-    __shared__ uint4 qb_lds[NW][NQK][2][64];
     __shared__ float comb[kSlots][NW][GW][D + 2];
     __shared__ float patch_val[NW][kTile][4];
     __shared__ int patch_flag[NW][kTile];
@@ -185,6 +184,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
 
     // ---- q' = clip(q) * scale * log2(e) of work item c (segment s) for this wave, and
     // the B operands of the QK MFMAs: column n < GW holds head n, split hi + lo ----
+    // score MFMA B operands (q' hi and lo) of the wave's current item, in registers
+    h8_t qreg[NQK][2];
     auto qprep = [&](const int s, const ItemCursor& c) {
         constexpr int E = D / 64;
         if (s >= kQStage) {
@@ -228,8 +229,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
                 hi8[j] = hi;
                 lo8[j] = (_Float16)(qv - (float)hi);
             }
-            qb_lds[wave][i][0][lane] = __builtin_bit_cast(uint4, hi8);
-            qb_lds[wave][i][1][lane] = __builtin_bit_cast(uint4, lo8);
+            qreg[i][0] = hi8;
+            qreg[i][1] = lo8;
         }
     };
 
@@ -324,8 +325,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
         f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < NQK; ++i) {
-            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[wave][i][0][lane]), sh, 0, 0, 0);
-            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), as_h8(qb_lds[wave][i][1][lane]), sl, 0, 0, 0);
+            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), qreg[i][0], sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(f.k[i]), qreg[i][1], sl, 0, 0, 0);
         }
         return sh + sl;
     };
