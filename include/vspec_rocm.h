@@ -188,11 +188,18 @@ const char* vspec_rocm_last_error(void);
 int vspec_rocm_device_count(void);
 
 /* The legacy contiguous-cache path (launch_attention with a host VspecKVCache*) keeps a
- * device mirror per cache so that each call uploads only the rows appended since the
- * previous one (kv_cache.c:160-226 appends only).  Call this when a cache is destroyed,
- * or when its rows are rewritten in place rather than appended (a shrunk current_tokens
- * or changed first/last synced rows are detected; other in-place edits are not), to free
- * the mirror's device memory; NULL releases every mirror.  Returns 1. */
+ * device mirror per cache.  By default every call uploads all current_tokens rows, as the
+ * reference's per-call copies do (cuda_attention_f32.cu:108-110), so any in-place edit of
+ * the caller's rows is seen.  A caller whose caches only grow by appends (kv_cache.c:160-226)
+ * may switch to uploading only the rows appended since the previous call; the mirror then
+ * still resyncs when current_tokens shrinks or the first or last synced row changes, but
+ * other in-place rewrites of earlier rows go unseen.  enable: 1 appends only, 0 every row,
+ * -1 back to the environment (VSPEC_ROCM_MIRROR_APPEND_ONLY, off when unset).  Process-wide;
+ * returns the previous setting (1/0).  No counterpart in the reference. */
+int vspec_rocm_cache_mirror_append_only(int enable);
+
+/* Free the device mirror of a cache (call when the cache is destroyed); NULL releases
+ * every mirror.  Returns 1. */
 int vspec_rocm_release_cache_mirror(const VspecKVCache* cache);
 
 /* ---- backend registry entry: replaces rocm_backend_stub.c:3-21 ----

@@ -487,6 +487,107 @@ def test_decode_custom_clamp_alpha(oracle, gpu, flag_gate, dtype, alpha):
     assert err <= tol_of(dtype, case_vmax(case))
 
 
+# ----------------------------------------------------------------------------- operand ranges
+# The matrix-core kernels feed q' (f16 and int4 pools) and, in the int4 kernel, p * V scale to
+# fp16 operands.  The reference computes in fp32/double over the whole float range
+# (attention_ref.c:50-79, three_bit_runtime_modules.c:175-250), so these cases put the operands
+# far outside fp16's range in both directions and compare with the oracle.
+
+
+def _decode_scaled(case, pool, dev, mode, scale=0.0, partition_tokens=0):
+    import torch
+    import vspec_rocm as vr
+
+    out = vr.paged_decode(pool, torch.from_numpy(case.tables).to(dev), torch.from_numpy(case.ctx).to(dev),
+                          torch.from_numpy(case.q).to(dev), max_ctx_len=case.tmax, numerics=mode, scale=scale,
+                          partition_tokens=partition_tokens)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+@pytest.mark.parametrize("D", [64, 128])
+def test_decode_huge_query_mode_p(oracle, gpu, flag_gate, dtype, D):
+    """Mode P has no +-16 clip, so q' = clip(q) * scale * log2(e) is unbounded: std(q) = 2e5
+    with a caller scale of 1.0 (D = 64) and std(q) = 3e6 with the default 1/sqrt(D) (D = 128)
+    put |q'| near 1e6 and 5e5, beyond fp16's 65504.  The oracle fixes scale = 1/sqrt(D); for
+    D = 64 it gets 8q, which the std clamp maps to 8 clip(q) exactly (a power of two scales the
+    double mean, variance and threshold exactly), so its scores equal the reference's on q with
+    scale 1.0 bit for bit."""
+    say(f"[huge q] dtype={dtype} D={D}")
+    case = make_case(oracle, dtype, 3, 8, 2, D, 16, [300, 77, 1], seed=131 + D + dtype, src16=False)
+    q = case.q.astype(np.float64)
+    if D == 64:
+        q_gpu = (q * 2e5).astype(np.float32)
+        case.q = (q_gpu * np.float32(8.0)).astype(np.float32)
+        scale = 1.0
+    else:
+        case.q = (q * 3e6).astype(np.float32)
+        q_gpu, scale = case.q, 0.0
+    pool = build_both(oracle, case, gpu)
+    want_q = case.q
+    case.q = q_gpu
+    got = _decode_scaled(case, pool, gpu, 0, scale=scale)
+    case.q = want_q
+    check_attention(oracle, case, got, 0)
+
+
+@pytest.mark.parametrize("dtype", [DTYPE_F32, DTYPE_F16, DTYPE_INT4])
+def test_decode_tiny_query_large_keys_mode_p(oracle, gpu, flag_gate, dtype):
+    """std(q) = 1e-4 against keys of std 1e4 (mode P): |q'| ~ 1e-5 lies in fp16's subnormal
+    range while the scores still spread over a few units, so q' must keep its relative
+    precision (the kernels shift it by a power of two before the hi + lo split)."""
+    say(f"[tiny q] dtype={dtype}")
+    case = make_case(oracle, dtype, 2, 16, 4, 128, 16, [400, 129], seed=141 + dtype, src16=False)
+    case.k_tokens = (case.k_tokens * np.float32(1e4)).astype(np.float32)
+    case.q = (case.q * np.float32(1e-4)).astype(np.float32)
+    pool = build_both(oracle, case, gpu)
+    got = run_decode(case, pool, gpu, 0)
+    # the scores do spread: the result is far from the plain mean of V
+    _, vals, _, _ = oracle.paged_gather(case.host, case.tables, case.ctx, out_mode=1)
+    mean0 = vals[: int(case.ctx[0]), 0].astype(np.float64).mean(axis=0)
+    assert np.abs(got[0, 0] - mean0).max() > 100 * TOL[DTYPE_F16]
+    check_attention(oracle, case, got, 0)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_decode_int4_large_v_scales(oracle, gpu, flag_gate, mode):
+    """int4 V groups with |v| ~ 1e4 (scales ~ 800-2000) under scores that climb by ~7.9 per 128
+    tokens: each wave of the int4 kernel takes every 8th tile pair of a range, so its lazy
+    running max trails its new scores by up to 2^7.9 and p * scale reaches ~4e5, which fp16
+    cannot hold.  The bound is relative: the north-star 4e-3 is stated for unit-scale data,
+    and the int4 kernel's P' rounding (relative 2^-12) scales with |v| (2.5e-4 max|v|)."""
+    say(f"[large v] mode={mode}")
+    D, Hq, Hkv = 128, 8, 2
+    G = Hq // Hkv
+    case = make_case(oracle, DTYPE_INT4, 2, Hq, Hkv, D, 16, [2049, 1500], seed=151, src16=False)
+    T = case.k_tokens.shape[1]
+    k = case.k_tokens.astype(np.float64)
+    t = np.arange(T, dtype=np.float64)
+    for b in range(case.B):
+        for hk in range(Hkv):
+            q0 = case.q[b, G * hk].astype(np.float64)
+            th = 4.5 * q0.std()
+            qc = np.clip(q0, -th, th)
+            u = q0 / np.linalg.norm(q0)
+            per_unit = float(u @ qc) / np.sqrt(D) * np.log2(np.e)  # log2 score per unit of a_t
+            a = (7.9 / 128.0) * t / per_unit
+            k[b, :, hk, :] = a[:, None] * u[None, :] + 0.05 * k[b, :, hk, :]
+    case.k_tokens = k.astype(np.float32)
+    case.v_tokens = (case.v_tokens * np.float32(3000.0)).astype(np.float32)
+    pool = build_both(oracle, case, gpu)
+    vmax = case_vmax(case)
+    assert vmax > 1e4
+    tol = 2.5e-4 * vmax + 2e-5
+    for pt in (0, 1024):
+        got = _decode_scaled(case, pool, gpu, mode, partition_tokens=pt)
+        want = oracle.paged_decode(mode, case.host, case.tables, case.ctx, case.q)
+        assert np.isfinite(got).all(), f"non-finite outputs (partition_tokens={pt})"
+        err = float(np.abs(got - want).max())
+        say(f"    partition_tokens={pt}: max-abs {err:.3e} (bound {tol:.2e}, outputs up to {np.abs(want).max():.1f})")
+        assert err <= tol
+
+
 @pytest.mark.parametrize("seed", range(24))
 def test_decode_random_shapes(oracle, gpu, seed):
     """Seeded random shapes against the oracle: pool dtype, batch 1-12, kv heads 1/2/4/8,
@@ -1505,10 +1606,57 @@ def test_backend_int3_cache_without_mirror(oracle, gpu, D, block_size, mode):
 def test_backend_decode_loop_appends_only(oracle, gpu, D):
     """A 64-step decode loop through the registry entry, as vspec_attention_forward
     (runtime.c:641-647) drives it: each step appends one token to the host VspecKVCache
-    (kv_cache.c:160-226) and calls launch_attention.  The device mirror uploads only the
-    appended rows; every step matches the oracle's attention_ref over all rows so far.
-    Then the cache is rewound (current_tokens shrinks) and refilled with other rows at the
-    same addresses: the mirror resyncs and the results follow the new rows."""
+    (kv_cache.c:160-226) and calls launch_attention.  With the append-only upload switched
+    on, the device mirror uploads only the appended rows; every step matches the oracle's
+    attention_ref over all rows so far.  Then the cache is rewound (current_tokens shrinks)
+    and refilled with other rows at the same addresses: the mirror resyncs and the results
+    follow the new rows."""
+    import ctypes as C
+    import vspec_rocm as vr
+
+    was = vr.lib().vspec_rocm_cache_mirror_append_only(1)
+    try:
+        _legacy_append_loop(oracle, D)
+    finally:
+        vr.lib().vspec_rocm_cache_mirror_append_only(-1)
+    assert was == 0  # off unless the caller or the environment turns it on
+
+
+@pytest.mark.parametrize("D", [128, 20])
+def test_backend_middle_row_rewrite(oracle, gpu, D):
+    """The default upload policy sends every row on every call, so a rewrite of rows in the
+    middle of a host VspecKVCache, with current_tokens unchanged and the first and last rows
+    untouched, is seen by the next launch_attention (the reference copies all rows per call,
+    cuda_attention_f32.cu:108-110): both calls match the oracle over the rows as they are."""
+    import ctypes as C
+    import vspec_rocm as vr
+
+    H, T = 4, 300
+    k = np.ascontiguousarray(oracle.normal(610 + D, T * H * D).reshape(T, H, D))
+    v = np.ascontiguousarray(oracle.normal(611 + D, T * H * D).reshape(T, H, D))
+    q = oracle.normal(612 + D, H * D).reshape(H, D) * 3
+    cache = vr.VspecKVCache()
+    cache.key, cache.value = k.ctypes.data, v.ctypes.data
+    cache.max_tokens, cache.num_heads, cache.head_dim, cache.current_tokens = T, H, D, T
+    assert vr.lib().vspec_rocm_cache_mirror_append_only(-1) == 0
+    try:
+        for mode in (0, 1):
+            out, err = _launch_cache(q, cache, mode)
+            want = oracle.attention_ref(mode, q, k, v)
+            assert np.abs(out - want).max() <= 2e-5, err
+            # rows 100-149 point at q (high scores) and carry large values
+            k[100:150] = q[None] * 0.5
+            v[100:150] *= 10.0
+            out2, err = _launch_cache(q, cache, mode)
+            want2 = oracle.attention_ref(mode, q, k, v)
+            assert np.abs(want2 - want).max() > 0.1  # the rewrite does change the result
+            assert np.abs(out2 - want2).max() <= 2e-5 * max(1.0, float(np.abs(want2).max())), err
+            k[:] = oracle.normal(610 + D + 17 * (mode + 1), T * H * D).reshape(T, H, D)
+    finally:
+        assert vr.lib().vspec_rocm_release_cache_mirror(C.cast(C.pointer(cache), C.c_void_p)) == 1
+
+
+def _legacy_append_loop(oracle, D):
     import ctypes as C
     import vspec_rocm as vr
 

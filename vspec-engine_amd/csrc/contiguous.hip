@@ -15,6 +15,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#include <strings.h>
 
 #include <mutex>
 
@@ -205,6 +206,18 @@ constexpr int kMirrors = 16;
 Mirror g_mirror[kMirrors];
 uint64_t g_mirror_clock = 0;
 std::mutex g_mirror_mu;
+// Upload policy of the mirror: -1 follows VSPEC_ROCM_MIRROR_APPEND_ONLY (unset, "0", "false",
+// "off", "no": whole cache), 0 uploads every row on every call, 1 only the rows appended
+// since the previous call (vspec_rocm_cache_mirror_append_only)
+int g_append_only = -1;
+
+bool append_only_mode() {
+    if (g_append_only >= 0) return g_append_only != 0;
+    const char* e = getenv("VSPEC_ROCM_MIRROR_APPEND_ONLY");
+    if (!e || !*e) return false;
+    return strcmp(e, "0") != 0 && strcasecmp(e, "false") != 0 && strcasecmp(e, "off") != 0 &&
+           strcasecmp(e, "no") != 0;
+}
 
 void mirror_free(Mirror& m) {
     if (m.paged) vspec_rocm_kv_pool_destroy(&m.kv);
@@ -327,6 +340,13 @@ Mirror* mirror_for(const VspecKVCache* c) {
 
 }  // namespace
 
+extern "C" int vspec_rocm_cache_mirror_append_only(int enable) {
+    std::lock_guard<std::mutex> lock(g_mirror_mu);
+    const int was = append_only_mode() ? 1 : 0;
+    g_append_only = enable < 0 ? -1 : (enable ? 1 : 0);
+    return was;
+}
+
 extern "C" int vspec_rocm_release_cache_mirror(const VspecKVCache* cache) {
     std::lock_guard<std::mutex> lock(g_mirror_mu);
     for (Mirror& m : g_mirror) {
@@ -380,9 +400,11 @@ extern "C" int vspec_rocm_attention_cache_host(const float* q, const VspecKVCach
     std::lock_guard<std::mutex> lock(g_mirror_mu);
     Mirror* m = mirror_for(cache);
     if (!m) return 0;
-    // resync from token 0 when the cache shrank or its synced rows changed
-    if (m->synced > tokens || (m->synced && (token_fingerprint(cache, ks, vs, 0) != m->fp_first ||
-                                              token_fingerprint(cache, ks, vs, m->synced - 1) != m->fp_last))) {
+    // Every row is uploaded again unless the caller promised appends only; even then the
+    // mirror resyncs from token 0 when the cache shrank or its first or last synced row changed.
+    if (!append_only_mode() || m->synced > tokens ||
+        (m->synced && (token_fingerprint(cache, ks, vs, 0) != m->fp_first ||
+                       token_fingerprint(cache, ks, vs, m->synced - 1) != m->fp_last))) {
         m->synced = 0;
     }
     const size_t t0 = m->synced, n = tokens - t0, H = heads, D = head_dim;

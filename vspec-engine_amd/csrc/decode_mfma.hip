@@ -11,6 +11,11 @@
 //                                                   hi + lo taken straight from the S^T
 //                                                   accumulator registers
 // Columns 0..GW-1 are the GQA query heads that share the tile; the rest stay zero.
+// q' of a head whose max |q'| lies outside [2^-4, 2^15) enters the MFMAs shifted by a power
+// of two (qnorm_shift), so that neither fp16 part overflows or loses its relative precision
+// in the subnormal range; the lane then keeps its scores in the shifted unit and takes the
+// factor back inside the exp2 argument.  p is at most 2^8 (lazy running max), so the P^T
+// operands stay in range whatever the data.
 //
 // The std clamp is screened per key from v_dot2 sums (sum x, sum x^2) and a packed
 // max|x|; keys it may affect (about 0.1% for N(0,1) data) get their scores recomputed
@@ -186,6 +191,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
     // the B operands of the QK MFMAs: column n < GW holds head n, split hi + lo ----
     // score MFMA B operands (q' hi and lo) of the wave's current item, in registers
     h8_t qreg[NQK][2];
+    // Head n's operands carry q' * 2^e_n (qnorm_shift), so the MFMAs return scores times
+    // 2^e_n.  The lane keeps them in that unit (raw) and so do its running max (m_raw), lazy
+    // threshold and clip bounds; qfac = 2^-e_n turns a raw difference into log2 units inside
+    // the exp2 argument, fma(s, qfac, -mf) with mf = m_raw * qfac, which costs no more than
+    // the subtraction it replaces and is exact in the power of two.
+    float qfac = 1.0f, qinv = 1.0f, thr_raw = 8.0f, clo_raw = -INFINITY, chi_raw = -INFINITY;
+    // score clip per lane: columns that hold no head clip to -inf (3-bit mode: +-24*log2e)
+    const float clip_hi = n < GW ? p.logit_clip : -INFINITY;
+    const float clip_lo = n < GW ? -p.logit_clip : -INFINITY;
     auto qprep = [&](const int s, const ItemCursor& c) {
         constexpr int E = D / 64;
         if (s >= kQStage) {
@@ -200,6 +214,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
             }
         }
         float (*src)[D] = s < kQStage ? qraw[s] : qs[wave];
+        int eh[GW];
 #pragma unroll
         for (int h = 0; h < GW; ++h) {
             float x[E];
@@ -214,9 +229,26 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
             for (int e = 0; e < E; ++e) v = fmaf(x[e] - mean, x[e] - mean, v);
             v = wave_sum(v);
             const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v * (1.0f / D))), p.input_clip);
+            float am = 0.f;
 #pragma unroll
-            for (int e = 0; e < E; ++e) qs[wave][h][lane * E + e] = fminf(fmaxf(x[e], -th), th) * p.qscale;
+            for (int e = 0; e < E; ++e) {
+                const float y = fminf(fmaxf(x[e], -th), th) * p.qscale;
+                qs[wave][h][lane * E + e] = y;
+                am = fmaxf(am, fabsf(y));
+            }
+            eh[h] = __builtin_amdgcn_readfirstlane(qnorm_shift(wave_max(am)));
         }
+        int en = 0;
+#pragma unroll
+        for (int h = 0; h < GW; ++h) en = n == h ? eh[h] : en;
+        qfac = pow2i(-en);
+        qinv = pow2i(en);
+        thr_raw = 8.0f * qinv;
+        clo_raw = clip_lo * qinv;
+        chi_raw = clip_hi * qinv;
+        // columns without a head get zero operands (the LDS read stays unconditional)
+        const int hn = n < GW ? n : 0;
+        const float qin = n < GW ? qinv : 0.0f;
         // this wave's own LDS writes are read back below: a wave's LDS accesses complete
         // in program order
 #pragma unroll
@@ -224,7 +256,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
             h8_t hi8, lo8;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float qv = n < GW ? qs[wave][n < GW ? n : 0][32 * i + 8 * g + j] : 0.f;
+                const float qv = qs[wave][hn][32 * i + 8 * g + j] * qin;
                 const _Float16 hi = (_Float16)qv;
                 hi8[j] = hi;
                 lo8[j] = (_Float16)(qv - (float)hi);
@@ -269,19 +301,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
     };
 
     f4_t acc[NDT];
-    // running max starts finite so exp2(s - m_run) is 0, never NaN, in the columns
-    // that hold no head (their scores stay -inf)
-    float m_run;
+    // Running max: m_raw in the lane's raw score unit starts at -inf, so the first valid
+    // score always moves it; mf = m_raw * qfac in log2 units starts finite, so that exp2 of
+    // a -inf score minus it is 0, never NaN, in columns that hold no head or no token yet.
+    float m_raw, mf;
     float l_run;  // sum of p for head n over this lane's tokens
     auto reset = [&]() {
 #pragma unroll
         for (int j = 0; j < NDT; ++j) acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
-        m_run = -1e30f;
+        m_raw = -INFINITY;
+        mf = -1e30f;
         l_run = 0.f;
     };
-    // score clip per lane: columns that hold no head clip to -inf (3-bit mode: +-24*log2e)
-    const float clip_hi = n < GW ? p.logit_clip : -INFINITY;
-    const float clip_lo = n < GW ? -p.logit_clip : -INFINITY;
     const h2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
 
     // Clamp screen of key n (this lane holds 8*NQK of its elements): mean and E[x^2]
@@ -373,7 +404,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 4 * g + r;
-                if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n];
+                if (patch_flag[wave][t]) sc[r] = patch_val[wave][t][n] * qinv;
             }
         }
     };
@@ -407,18 +438,19 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
         // cross-lane max is taken only then. ----
         float s[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s[r] = __builtin_amdgcn_fmed3f(sc[r], clip_lo, clip_hi);
+        for (int r = 0; r < 4; ++r) s[r] = __builtin_amdgcn_fmed3f(sc[r], clo_raw, chi_raw);
         if (nvalid < kTile) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) s[r] = 4 * g + r < nvalid ? s[r] : -INFINITY;
             clear_masked_v(f, nvalid);
         }
         const float smax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        if (__builtin_amdgcn_ballot_w64(smax > m_run + 8.0f) != 0) {
+        if (__builtin_amdgcn_ballot_w64(smax > m_raw + thr_raw) != 0) {
             const float mt = max_rows(smax);
-            const bool need = mt > m_run + 8.0f;
-            const float fct = need ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;
-            m_run = need ? mt : m_run;
+            const bool need = mt > m_raw + thr_raw;
+            const float fct = need ? __builtin_amdgcn_exp2f((m_raw - mt) * qfac) : 1.0f;
+            m_raw = need ? mt : m_raw;
+            mf = need ? mt * qfac : mf;
             l_run *= fct;
 #pragma unroll
             for (int j = 0; j < NDT; ++j) acc[j] *= fct;
@@ -427,7 +459,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
         h4_t phi, plo;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(s[r] - m_run);
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], qfac, -mf));
             l_run += pv;
             const _Float16 hi = (_Float16)pv;
             phi[r] = hi;
@@ -460,7 +492,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
                 for (int r = 0; r < 4; ++r) comb[slot][wave][n][2 + 16 * j + 4 * g + r] = acc[j][r];
             }
             if (g == 0) {
-                comb[slot][wave][n][0] = m_run;
+                comb[slot][wave][n][0] = mf;
                 comb[slot][wave][n][1] = l;
             }
         }

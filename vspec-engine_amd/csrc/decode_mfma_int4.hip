@@ -19,6 +19,11 @@
 //     d.  The V pool is stored in 16-token tiles whose lane chunks are half of these A
 //     operands.
 //
+// Operand ranges: q' of a head whose max |q'| lies outside [2^-4, 2^15) enters the score
+// MFMAs shifted by a power of two (qnorm_shift), taken back out of the scores; P' = p * scale
+// stays below 65504 because p <= 2^thr and a tile pair holding a V scale at or above
+// 2^(16 - thr) first lowers thr (and moves the softmax reference point up by the same amount).
+//
 // A nibble t (two's complement code c = (t ^ 8) - 8) becomes an exact fp16 through a
 // magic exponent, two codes per 32-bit operation, plus a bias that the MFMAs cancel
 // (biased_codes_to_f16).
@@ -38,6 +43,19 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+template <bool B>
+struct BoolTag {
+    static constexpr bool value = B;
+};
+
+// fp16 bits of 2^(16 - thr) minus one, in both halves: a V scale s reaches that bound exactly
+// when the saturating difference s - (bits - 1) is nonzero
+__device__ __forceinline__ u16x2 vscale_bound_bits(int thr) {
+    const unsigned short b = (unsigned short)(((31 - thr) << 10) - 1);
+    return u16x2{b, b};
+}
 
 // Four fp16 pairs from one code dword: pair k = (nibble k, nibble k + 4).  A nibble t
 // sits in an fp16 mantissa under a magic exponent (1024 + u for bits 0..3, 64 + u for
@@ -159,6 +177,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
     __shared__ float qs[GW][D];
     __shared__ uint4 qb_lds[NQ][2][64];  // QK B operands (hi, lo) per lane
     __shared__ float kbias_lds[16];       // per score column: the K bias' share (k_codes_to_f16)
+    __shared__ int qexp_lds[4];           // per head: the q' operand shift (qnorm_shift)
     __shared__ float patch_val[kWaves][kTile][4];
     __shared__ int patch_flag[kWaves][kTile];
     __shared__ SplitShared split_sh;
@@ -499,8 +518,15 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             for (int e = 0; e < E; ++e) v = fmaf(x[e] - mean, x[e] - mean, v);
             v = wave_sum(v);
             const float th = fminf(fmaxf(1e-6f, p.alpha * sqrtf(v * (1.0f / D))), p.input_clip);
+            float am = 0.f;
 #pragma unroll
-            for (int e = 0; e < E; ++e) qs[wave][lane * E + e] = fminf(fmaxf(x[e], -th), th) * p.qscale;
+            for (int e = 0; e < E; ++e) {
+                const float y = fminf(fmaxf(x[e], -th), th) * p.qscale;
+                qs[wave][lane * E + e] = y;
+                am = fmaxf(am, fabsf(y));
+            }
+            am = wave_max(am);
+            if (lane == 0) qexp_lds[wave] = qnorm_shift(am);
         }
         // The first ST pairs are on their way while the q operands are prepared (after the
         // q rows are in registers: a wait for those would also wait for these).
@@ -521,8 +547,13 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 
         // ---- QK B operands: k-slots 8g..8g+7 of MFMA m carry code dword dw = g*NQ + m in
         // the order e = 0,4,1,5,2,6,3,7; column n takes group n/4 of head n%4 ----
+        // head h's operands carry q' * 2^e_h (qnorm_shift), taken back out of the scores by
+        // qfac = 2^-e_h; the tile loop is instantiated twice, and only the one run for items
+        // where some head has e != 0 (qnorm, wave-uniform) multiplies
         if (wave == 0) {
             const int hh = n & 3;
+            const int hs = hh < GW ? hh : 0;
+            const float qin = pow2i(qexp_lds[hs]);
             float odd = 0.f;  // this lane's B operands on the k-slots of odd elements
 #pragma unroll
             for (int m = 0; m < NQ; ++m) {
@@ -532,7 +563,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int e = (j >> 1) + 4 * (j & 1);
-                    const float qv = on ? qs[hh < GW ? hh : 0][8 * dw + e] : 0.f;
+                    const float qv = qs[hs][8 * dw + e] * (on ? qin : 0.0f);
                     const _Float16 hi = (_Float16)qv;
                     hi8[j] = hi;
                     lo8[j] = (_Float16)(qv - (float)hi);
@@ -546,6 +577,11 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         }
         __syncthreads();
         const float kbias = kbias_lds[n];
+        int qe_any = 0;
+#pragma unroll
+        for (int h = 0; h < GW; ++h) qe_any |= qexp_lds[h];
+        const bool qnorm = __builtin_amdgcn_readfirstlane(qe_any) != 0;
+        const float qfac = (n & 3) < GW ? pow2i(-qexp_lds[(n & 3) < GW ? (n & 3) : 0]) : 1.0f;
         // the B operands stay in registers for the whole item (32 VGPRs): read from LDS per
         // pair they cost 8 reads and a wait before each score MFMA
         h8_t qreg[NQ][2];
@@ -570,6 +606,11 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         float clip_hi = head_col ? p.logit_clip : -INFINITY;
         float clip_lo = head_col ? -p.logit_clip : -INFINITY;
         bool first = true;
+        // p = exp2(s) stays at or below 2^thr (the lazy max below), so P' = p * (V scale) stays
+        // below 65504 while every V scale is below 2^(16 - thr); vtb holds that bound's fp16
+        // bits minus one, twice (see pv)
+        int thr = 8;
+        u16x2 vtb = vscale_bound_bits(thr);
         // every column holds a head and the logits are not clipped: the clip is the identity
         const bool clip_on = GW < 4 || p.logit_clip < INFINITY;
 
@@ -610,7 +651,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // bias' share of the column (its magnitude, 72 |sum q'|, costs 2^-24 of it); each of the four
         // group columns of a head is scaled by its fp16 K scale and takes a quarter of
         // m_run in the same mixed-precision FMA, so the column sum is score - m_run.
-        auto qk = [&](const I4Frags<D>& f) -> f4_t {
+        auto qk = [&](const I4Frags<D>& f, auto qn) -> f4_t {
             f4_t sacc = {-kbias, -kbias, -kbias, -kbias};
 #pragma unroll
             for (int m = 0; m < NQ; ++m) {
@@ -620,6 +661,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                 sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qreg[m][0], sacc, 0, 0, 0);
                 sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qreg[m][1], sacc, 0, 0, 0);
             }
+            if constexpr (decltype(qn)::value) sacc *= qfac;
             const h2_t kc[2] = {__builtin_bit_cast(h2_t, f.ks_col.x), __builtin_bit_cast(h2_t, f.ks_col.y)};
             const float mq = -0.25f * m_run;
             f4_t sc;
@@ -691,7 +733,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // Two tiles per step: k-slot 8g + i of the PV MFMA is token 4g + i of tile A (i < 4)
         // or token 4g + i - 4 of tile B.
         // Scores and softmax weights of a pair (the V half of the fragments is not read yet).
-        auto scores = [&](I4Frags<D>& fa, I4Frags<D>& fb, const int nva, const int nvb, const int tile_a,
+        auto scores = [&](auto qn, I4Frags<D>& fa, I4Frags<D>& fb, const int nva, const int nvb, const int tile_a,
                           float (&pr)[8]) {
             // clamp flags: from the pool, or from the screen (both tiles in one basic block:
             // their chains interleave)
@@ -706,13 +748,13 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             if (scr_a || scr_b) {
                 const Screen sna = screen(fa, nva);
                 const Screen snb = screen(fb, nvb);
-                sa = qk(fa);
-                sb = qk(fb);
+                sa = qk(fa, qn);
+                sb = qk(fb, qn);
                 fla = scr_a ? tokens(__builtin_amdgcn_ballot_w64(sna.flag)) : word_of(fa) & valid_mask(nva);
                 flb = scr_b ? tokens(__builtin_amdgcn_ballot_w64(snb.flag)) : word_of(fb) & valid_mask(nvb);
             } else {
-                sa = qk(fa);
-                sb = qk(fb);
+                sa = qk(fa, qn);
+                sb = qk(fb, qn);
                 fla = word_of(fa) & valid_mask(nva);
                 flb = word_of(fb) & valid_mask(nvb);
             }
@@ -745,11 +787,11 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             float smax = s[0];
 #pragma unroll
             for (int i = 1; i < 8; ++i) smax = fmaxf(smax, s[i]);
-            if (first || __builtin_amdgcn_ballot_w64(smax > 8.0f) != 0) {
+            if (first || __builtin_amdgcn_ballot_w64(smax > (float)thr) != 0) {
                 const float mt = max_rows(smax);
                 // columns without a head (all -inf) do not move; the four columns of a head
                 // (each subtracts a quarter of its own m_run in qk) take the same move
-                const bool need = first ? mt > -INFINITY : mt > 8.0f;
+                const bool need = first ? mt > -INFINITY : mt > (float)thr;
                 const float dm = need ? mt : 0.0f;
                 const float fct = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
                 m_run += dm;
@@ -775,9 +817,41 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                               (_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1032.0f};
         const h8_t bias_hi = {(_Float16)-72.0f, (_Float16)-72.0f, (_Float16)-72.0f, (_Float16)-72.0f,
                               (_Float16)-72.0f, (_Float16)-72.0f, (_Float16)-72.0f, (_Float16)-72.0f};
-        auto pv = [&](I4Frags<D>& fa, I4Frags<D>& fb, const int nva, const int nvb, const float (&pr)[8]) {
+        auto pv = [&](I4Frags<D>& fa, I4Frags<D>& fb, const int nva, const int nvb, float (&pr)[8], const uint32_t vsw) {
             clear_masked_scales(fa, nva);
             clear_masked_scales(fb, nvb);
+
+            // A V scale of the pair at or above 2^(16 - thr) (checked on the stage's raw scale
+            // bits: garbage past a context only costs the exact check) may overflow P'.  Then
+            // thr drops to 15 - X, X = floor(log2) of the largest valid scale of the pair, and
+            // the reference point m_run moves up by the difference: acc, l_run and this pair's
+            // p scale by the same power of two, so acc / l_run is unchanged.
+            const u16x2 over = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, vsw), vtb);
+            if (__builtin_amdgcn_ballot_w64(__builtin_bit_cast(uint32_t, over) != 0u) != 0) {
+                float vm = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) vm = fmaxf(vm, fmaxf((float)fa.vs[r], (float)fb.vs[r]));
+                vm = wave_max(vm);
+                // vm in [2^X, 2^(X + 1)); vm = 0 gives X = -1
+                int X;
+                (void)frexpf(vm, &X);
+                X -= 1;
+                const int tnew = __builtin_amdgcn_readfirstlane(min(thr, 15 - X));
+                if (tnew < thr) {
+                    const int dl = thr - tnew;
+                    const float f = pow2i(-dl);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) pr[i] *= f;
+                    l_run *= f;
+#pragma unroll
+                    for (int j = 0; j < NDT; ++j) acc[j] *= f;
+                    m_run += (float)dl;
+                    clip_lo -= (float)dl;
+                    clip_hi -= (float)dl;
+                    thr = tnew;
+                    vtb = vscale_bound_bits(thr);
+                }
+            }
 
             // P' = p * scale rounded once to fp16 (v_fma_mix, relative error <= 2^-12): the
             // output error stays below 2.4e-4 * max|v|.  Column n carries the V scales of
@@ -801,43 +875,50 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
             }
         };
 
-        for (int tile = t0; tile < tile_end; tile += ST * step) {
+        auto tile_loop = [&](auto qn) {
+            for (int tile = t0; tile < tile_end; tile += ST * step) {
 #pragma unroll
-            for (int u = 0; u < ST; ++u) {
-                const int t = tile + u * step;
-                if (t >= tile_end) break;
-                // the oldest pair in flight is this one
-                wait_loads<kLoadsPerPair * (ST - 1)>();
-                I4Frags<D> fa, fb;
-                fa.flags = flag_s[u][0];
-                fa.fword = fword_s[u][0];
-                fb.flags = flag_s[u][1];
-                fb.fword = fword_s[u][1];
-                const int capa = cap_s[u][0], capb = cap_s[u][1];
-                const int nva = max(0, min(capa, ctx - t * kTile));
-                const int nvb = max(0, min(capb, ctx - (t + 1) * kTile));
-                const bool live = capa > 0 || capb > 0;
-                float pr[8];
-                if (nt_item && (t == U - 1 || t + 1 == U - 1)) {
-                    patch_new_token(stg[u][wave], t == U - 1 ? 0 : 1);
-                    // nt's clamp flag bit in its tile's flag word
-                    if (t == U - 1) fa.flags = (fa.flags & ~nt_bit) | nt_val;
-                    else fb.flags = (fb.flags & ~nt_bit) | nt_val;
+                for (int u = 0; u < ST; ++u) {
+                    const int t = tile + u * step;
+                    if (t >= tile_end) break;
+                    // the oldest pair in flight is this one
+                    wait_loads<kLoadsPerPair * (ST - 1)>();
+                    I4Frags<D> fa, fb;
+                    fa.flags = flag_s[u][0];
+                    fa.fword = fword_s[u][0];
+                    fb.flags = flag_s[u][1];
+                    fb.fword = fword_s[u][1];
+                    const int capa = cap_s[u][0], capb = cap_s[u][1];
+                    const int nva = max(0, min(capa, ctx - t * kTile));
+                    const int nvb = max(0, min(capb, ctx - (t + 1) * kTile));
+                    const bool live = capa > 0 || capb > 0;
+                    float pr[8];
+                    uint32_t vsw = 0u;
+                    if (nt_item && (t == U - 1 || t + 1 == U - 1)) {
+                        patch_new_token(stg[u][wave], t == U - 1 ? 0 : 1);
+                        // nt's clamp flag bit in its tile's flag word
+                        if (t == U - 1) fa.flags = (fa.flags & ~nt_bit) | nt_val;
+                        else fb.flags = (fb.flags & ~nt_bit) | nt_val;
+                    }
+                    if (live) {
+                        fetch_k(stg[u][wave], 0, fa);
+                        fetch_k(stg[u][wave], 1, fb);
+                        scores(qn, fa, fb, nva, nvb, t, pr);
+                        fetch_v(stg[u][wave], 0, fa);
+                        fetch_v(stg[u][wave], 1, fb);
+                        // raw V scale bits of the pair: lanes 0-31 tile a, 32-63 tile b
+                        vsw = (lane & 31) < 8 * NG ? stg[u][wave].sc[lane >> 5][32 + (lane & 31)] : 0u;
+                    }
+                    // the stage is read: reload it with the pair ST steps ahead
+                    wait_lds_reads();
+                    issue(t + ST * step, u, next);
+                    next = lookup(t + (ST + 1) * step);
+                    if (live) pv(fa, fb, nva, nvb, pr, vsw);
                 }
-                if (live) {
-                    fetch_k(stg[u][wave], 0, fa);
-                    fetch_k(stg[u][wave], 1, fb);
-                    scores(fa, fb, nva, nvb, t, pr);
-                    fetch_v(stg[u][wave], 0, fa);
-                    fetch_v(stg[u][wave], 1, fb);
-                }
-                // the stage is read: reload it with the pair ST steps ahead
-                wait_lds_reads();
-                issue(t + ST * step, u, next);
-                next = lookup(t + (ST + 1) * step);
-                if (live) pv(fa, fb, nva, nvb, pr);
             }
-        }
+        };
+        if (qnorm) tile_loop(BoolTag<true>{});
+        else tile_loop(BoolTag<false>{});
         // every load has landed before the ring is reused (the wave results below share
         // its memory) or the wave ends
         wait_loads<0>();

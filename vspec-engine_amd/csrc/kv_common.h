@@ -167,6 +167,31 @@ __device__ __forceinline__ float group_sum(float x) {
 // full-wave sum (every lane gets it)
 __device__ __forceinline__ float wave_sum(float x) { return add_rows(group_sum<16>(x)); }
 
+// full-wave max (every lane gets it)
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<kQuadXor1>(x));
+    x = fmaxf(x, dpp<kQuadXor2>(x));
+    x = fmaxf(x, dpp<kRowHalfMirror>(x));
+    x = fmaxf(x, dpp<kRowMirror>(x));
+    return max_rows(x);
+}
+
+// Power-of-two shift e of a score operand row (q' of one query head) before its fp16 hi + lo
+// split: the MFMAs read q' * 2^e and the scores are multiplied by 2^-e, both exact.  amax is
+// max |q'| of the row.  Rows with amax in [2^-4, 2^15) keep e = 0: hi stays below 65504, and
+// lo's fp16 rounding (absolute 2^-25 where lo is subnormal) stays within 2^-21 of amax.  Other
+// rows move to amax * 2^e in [2^14, 2^15); e is clamped to +-100 so that 2^e and 2^-e are
+// normal floats.  amax = 0, inf or NaN keeps e = 0.
+__device__ __forceinline__ int qnorm_shift(float amax) {
+    if (!(amax > 0.f) || !(amax < INFINITY) || (amax >= 0.0625f && amax < 32768.0f)) return 0;
+    // amax in [2^(x-1), 2^x)
+    int x;
+    (void)frexpf(amax, &x);
+    return min(max(15 - x, -100), 100);
+}
+// 2^e for e in [-126, 127]
+__device__ __forceinline__ float pow2i(int e) { return __builtin_bit_cast(float, (e + 127) << 23); }
+
 // Max over the 64/N groups of a wave when x is uniform inside each aligned group of N.
 template <int N>
 __device__ __forceinline__ float max_across_groups(float x) {

@@ -164,6 +164,7 @@ SIGNATURES = {
     "vspec_rocm_device_count": (C.c_int, []),
     "vspec_rocm_backend_available": (C.c_int, []),
     "vspec_rocm_release_cache_mirror": (C.c_int, [_vp]),
+    "vspec_rocm_cache_mirror_append_only": (C.c_int, [C.c_int]),
     "vspec_make_rocm_backend": (VspecBackend, []),
     # include/vspec_rocm_paged.h
     "vspec_rocm_paged_meta_create": (_vp, [C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t]),
