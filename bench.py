@@ -43,6 +43,8 @@ WORKLOADS = {
     "qwen3-8b-b64-ctx4k": dict(B=64, T=4097, Hq=32, Hkv=8, D=128, P=16, dtype="f16"),
     "qwen3-8b-b16-ctx2k": dict(B=16, T=2049, Hq=32, Hkv=8, D=128, P=16, dtype="f16"),
     "qwen3-8b-b16-ctx2k-int4": dict(B=16, T=2049, Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
+    # the reference cache's own element type (kv_paged_cache.h:7-49): fp32 pools
+    "qwen3-8b-b16-ctx2k-f32": dict(B=16, T=2049, Hq=32, Hkv=8, D=128, P=16, dtype="f32"),
     "qwen3-8b-b64-ctx4k-int4": dict(B=64, T=4097, Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
     "qwen3-8b-b64-ctx128-8k": dict(B=64, ctx_range=(128, 8192), Hq=32, Hkv=8, D=128, P=16, dtype="f16"),
     "qwen3-8b-b64-ctx128-8k-int4": dict(B=64, ctx_range=(128, 8192), Hq=32, Hkv=8, D=128, P=16, dtype="int4"),
@@ -447,6 +449,59 @@ def run_legacy(args):
                     "released: the mirror is released before each call"}
 
 
+def run_plan(args):
+    """Host step planning for a steady decode batch: 64 sequences at 4k-token contexts in
+    16-token pages, one new token each per step.  Times vspec_rocm_paged_plan_step (tables
+    written whole every step) against vspec_rocm_paged_plan_step_update (tables kept between
+    steps, changed entries only), both with per-entry used counts, one ctypes call per step
+    on one host thread.  Needs no GPU."""
+    import ctypes as C
+
+    import numpy as np
+
+    import vspec_rocm as vr
+
+    B, T, P = 64, args.ctx or 4096, 16
+    steps = max(args.steps, 200)
+    n_calls = steps + args.warmup
+    max_blocks = (T + n_calls + P - 1) // P + 1
+    L = vr.lib()
+    p32 = lambda a: a.ctypes.data_as(C.POINTER(C.c_int32))
+    out = {}
+    for kind, fn in (("whole", L.vspec_rocm_paged_plan_step), ("update", L.vspec_rocm_paged_plan_step_update)):
+        m = L.vspec_rocm_paged_meta_create(P, B * max_blocks + 64, 0, max_blocks)
+        tables = np.full((B, max_blocks), -1, np.int32)
+        used = np.zeros((B, max_blocks), np.int32)
+        ctx = np.zeros(B, np.int32)
+        start = np.zeros(B, np.int32)
+        titem = np.zeros(B * T, np.int32)
+        tpos = np.zeros(B * T, np.int32)
+        got = C.c_size_t()
+        ptrs = [p32(a) for a in (tables, used, ctx, start, titem, tpos)]
+        prefill = (vr.VspecRocmStepItem * B)(*[vr.VspecRocmStepItem(i + 1, 1, T - 1, 0) for i in range(B)])
+        decode = (vr.VspecRocmStepItem * B)(*[vr.VspecRocmStepItem(i + 1, 2, 1, T - 1) for i in range(B)])
+        try:
+            assert fn(m, prefill, B, ptrs[0], ptrs[1], max_blocks, ptrs[2], ptrs[3], ptrs[4], ptrs[5], B * T,
+                      C.byref(got))
+            for _ in range(args.warmup):
+                assert fn(m, decode, B, ptrs[0], ptrs[1], max_blocks, ptrs[2], ptrs[3], ptrs[4], ptrs[5], B * T,
+                          C.byref(got))
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn(m, decode, B, ptrs[0], ptrs[1], max_blocks, ptrs[2], ptrs[3], ptrs[4], ptrs[5], B * T, C.byref(got))
+            out[kind] = (time.perf_counter() - t0) / steps * 1e6
+            assert int(ctx[0]) == T - 1 + args.warmup + steps
+        finally:
+            L.vspec_rocm_paged_meta_destroy(m)
+    return {"metric": "host step planning, 64-sequence decode step", "value": out["update"], "unit": "us/step",
+            "higher_is_better": False, "n_gpus": 0, "steps": steps,
+            "config": {"workload": f"plan-b{B}-ctx{T}", "batch": B, "ctx": T, "page_tokens": P,
+                       "tables": "block ids + per-entry used counts"},
+            "whole_us_per_step": out["whole"], "update_us_per_step": out["update"],
+            "note": "whole: vspec_rocm_paged_plan_step writes every row; update: vspec_rocm_paged_plan_step_update "
+                    "writes the entries that changed; one ctypes call per step, one host thread"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -464,6 +519,8 @@ def main():
                     help="print the HBM bandwidth probes (copy, random/sequential tile reads) and exit")
     ap.add_argument("--no-probe", action="store_true",
                     help="skip the probe ceilings in the bench line")
+    ap.add_argument("--plan", action="store_true",
+                    help="time the host step planner (64 sequences, --ctx tokens, default 4096) and exit; no GPU")
     ap.add_argument("--legacy", action="store_true",
                     help="time the legacy registry path (launch_attention over a host VspecKVCache) and exit")
     ap.add_argument("--legacy-tokens", type=int, default=4096)
@@ -484,6 +541,10 @@ def main():
               "path shards by sequence or kv head with no exchange; see DESIGN.md). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.plan:
+        print(json.dumps(run_plan(args)), flush=True)
+        return
 
     import torch
 

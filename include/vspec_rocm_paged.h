@@ -107,6 +107,19 @@ int vspec_rocm_paged_plan_step(VspecRocmPagedMeta* m, const VspecRocmStepItem* i
                                size_t max_blocks, int32_t* ctx_lens, int32_t* start_pos,
                                int32_t* token_item, int32_t* token_pos, size_t max_tokens,
                                size_t* n_tokens);
+/* vspec_rocm_paged_plan_step for a serving loop that keeps its host tables between steps:
+ * pass the same block_tables / block_used buffers (and max_blocks) every step and leave
+ * their contents as the previous call wrote them.  A row that the previous call wrote for
+ * the same session (not evicted and reopened since) only gets the entries that changed:
+ * the former last entry's used count and the pages opened since; other rows are written
+ * whole.  Outputs and failures are those of vspec_rocm_paged_plan_step; on a failure the
+ * rows written so far stay consistent with what the next call assumes.  No counterpart in
+ * the reference (its callers append token by token, kv_paged_cache.c:243-310). */
+int vspec_rocm_paged_plan_step_update(VspecRocmPagedMeta* m, const VspecRocmStepItem* items,
+                                      size_t n_items, int32_t* block_tables, int32_t* block_used,
+                                      size_t max_blocks, int32_t* ctx_lens, int32_t* start_pos,
+                                      int32_t* token_item, int32_t* token_pos, size_t max_tokens,
+                                      size_t* n_tokens);
 
 /* Append packed new tokens (device pointers): token t of k_new/v_new ([n][H][D] in
  * src_dtype) goes to position token_pos[t] of the sequence whose block table is row

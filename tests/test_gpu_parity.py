@@ -664,10 +664,12 @@ def test_config2_3_qwen_decode(oracle, gpu, flag_gate, dtype, mode):
 
 def test_config4_continuous_batching(oracle, gpu):
     """C4: B=64, context ~ U[128, 8192], fragmented tables from a 1.2x pool (fp16).
-    The oracle checks 12 sequences including the shortest and the longest."""
+    The whole pool (both sides appended token by token) is compared byte for byte; the
+    oracle's attention checks 12 sequences including the shortest and the longest."""
     say("[c4] build")
     case = continuous_c4(oracle)
     pool = build_both(oracle, case, gpu, prefix_split=False)
+    assert_pools_equal(case.host, pool)
     order = np.argsort(case.ctx)
     subset = sorted(set(order[:4].tolist() + order[-4:].tolist() + [0, 1, 31, 63]))
     for pt in (0, 256):
@@ -1232,7 +1234,9 @@ def test_full_size_sampled_against_oracle(oracle, gpu, shape, dtype):
     appends each sequence's last token and attends (mode R), then a plain decode runs
     in mode P.  Four sampled sequences are gathered back (dequantised for int4), laid into
     an fp32 oracle pool and decoded by the oracle: the GPU rows must agree within the
-    tolerance of the pool dtype."""
+    tolerance of the pool dtype.  The append is checked on its own as well: the sampled
+    sequences' fp16 source rows (context and decode token) go through the oracle's append
+    into a pool of their own, whose raw gather must equal the GPU's byte for byte."""
     import torch
     import vspec_rocm as vr
 
@@ -1253,12 +1257,16 @@ def test_full_size_sampled_against_oracle(oracle, gpu, shape, dtype):
         tab[b, : nb[b]] = perm[off: off + nb[b]]
         off += int(nb[b])
     T = int(ctx.max())
+    sample = np.array([0, 17, 42, 63])
+    src = {}
     for b in range(B):
         # each sequence's context minus the decode token, in one append launch per sequence
         n = int(ctx[b]) - 1
         k = torch.randn((1, n, Hkv, D), generator=g, device=gpu).to(torch.float16)
         v = torch.randn((1, n, Hkv, D), generator=g, device=gpu).to(torch.float16)
         vr.kv_append(pool, tab[b: b + 1], torch.zeros(1, dtype=torch.int32, device=gpu), k, v)
+        if b in sample:
+            src[b] = (_f16_bits(k), _f16_bits(v))
     kn = torch.randn((B, Hkv, D), generator=g, device=gpu).to(torch.float16)
     vn = torch.randn((B, Hkv, D), generator=g, device=gpu).to(torch.float16)
     q = torch.randn((B, Hq, D), generator=g, device=gpu)
@@ -1266,7 +1274,13 @@ def test_full_size_sampled_against_oracle(oracle, gpu, shape, dtype):
     got = {1: vr.paged_decode_step(pool, tab, cl, q, kn, vn, max_ctx_len=T, numerics=1).cpu().numpy()}
     got[0] = vr.paged_decode(pool, tab, cl, q, max_ctx_len=T, numerics=0).cpu().numpy()
     torch.cuda.synchronize()
-    sample = np.array([0, 17, 42, 63])
+    kn_b, vn_b = _f16_bits(kn), _f16_bits(vn)
+    for b in sample:
+        n = int(ctx[b])
+        chunks = [(src[b][0], src[b][1], 0), (kn_b[b][None, None], vn_b[b][None, None], n - 1)]
+        _check_raw_gather_against_oracle(oracle, pool, tab[b: b + 1], cl[b: b + 1], dtype, P, Hkv, D, chunks,
+                                         np.arange((n + P - 1) // P, dtype=np.int32), n)
+    say(f"[full-size] append of sequences {sample.tolist()} byte-exact")
     st = torch.from_numpy(sample).to(gpu)
     kf, vf, _, _ = vr.kv_gather(pool, tab[st], cl[st], out_mode=vr.GATHER_F32, max_ctx_len=T)
     kf, vf = kf.cpu().numpy(), vf.cpu().numpy()
@@ -1278,6 +1292,36 @@ def test_full_size_sampled_against_oracle(oracle, gpu, shape, dtype):
         say(f"[full-size] mode={mode} max-abs {err:.2e} (bound {tol:.1e})")
         assert np.isfinite(got[mode]).all()
         assert err <= tol
+
+
+def _f16_bits(t):
+    return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+
+def _check_raw_gather_against_oracle(oracle, pool, tab_row, ctx_row, dtype, P, Hkv, D, chunks, table, ctx,
+                                     pool_blocks=None):
+    """One sequence at full size: the oracle appends `chunks` ((k, v, start) of fp16 bits,
+    [1][n][Hkv][D]) into a pool of its own through the identity table, then gathers `ctx`
+    tokens through `table`; the GPU's raw gather of the sequence must hold the same bytes."""
+    import vspec_rocm as vr
+
+    nblk = pool_blocks if pool_blocks is not None else int(table.size)
+    host = HostPool(dtype, nblk, P, Hkv, D)
+    ident = np.arange(nblk, dtype=np.int32)[None, :]
+    for k, v, start in chunks:
+        assert oracle.paged_append(host, ident, np.array([start], np.int32), np.ascontiguousarray(k),
+                                   np.ascontiguousarray(v))
+    want = oracle.paged_gather(host, table[None, :].astype(np.int32), np.array([ctx], np.int32), out_mode=0)
+    got = vr.kv_gather(pool, tab_row, ctx_row, out_mode=vr.GATHER_RAW, max_ctx_len=ctx)
+    for name, g_, w_ in zip(("k", "v", "k_scales", "v_scales"), got, want):
+        if w_ is None:
+            assert g_ is None
+            continue
+        gb = np.ascontiguousarray(g_.cpu().numpy()).view(np.uint8).reshape(-1)
+        wb = np.ascontiguousarray(w_).view(np.uint8).reshape(-1)
+        assert gb.size == wb.size, name
+        bad = np.flatnonzero(gb != wb)
+        assert bad.size == 0, f"{name}: {bad.size} bytes differ (first at byte {bad[0]})"
 
 
 def test_config5_full_size_sampled(oracle, gpu):
@@ -1295,11 +1339,14 @@ def test_config5_full_size_sampled(oracle, gpu):
     g.manual_seed(55)
     pool = vr.PagedPool(DTYPE_INT4, plan["num_blocks"], P, Hkv, D, device=gpu)
     tab = torch.from_numpy(plan["tables"]).to(gpu)
+    src = {}
     for b in range(B):
         n = int(plan["L0"][b])
         k = torch.randn((1, n, Hkv, D), generator=g, device=gpu).to(torch.float16)
         v = torch.randn((1, n, Hkv, D), generator=g, device=gpu).to(torch.float16)
         vr.kv_append(pool, tab[b: b + 1], torch.zeros(1, dtype=torch.int32, device=gpu), k, v)
+        if b in (0, 5):
+            src[b] = (_f16_bits(k), _f16_bits(v))
     kc = torch.randn((B, chunk, Hkv, D), generator=g, device=gpu).to(torch.float16)
     vc = torch.randn((B, chunk, Hkv, D), generator=g, device=gpu).to(torch.float16)
     vr.kv_append(pool, tab, torch.from_numpy(plan["L0"]).to(gpu), kc, vc)
@@ -1310,6 +1357,15 @@ def test_config5_full_size_sampled(oracle, gpu):
     T = int(plan["new_ctx"].max())
     got = {m: vr.paged_decode(pool, ntab, ncl, q, max_ctx_len=T, numerics=m).cpu().numpy() for m in (1, 0)}
     sample = np.array([0, 5])
+    # the sampled sequences' chunk append, eviction and compaction, independently: the oracle
+    # appends their source rows into a pool of their own and keeps the surviving blocks
+    kc_b, vc_b = _f16_bits(kc), _f16_bits(vc)
+    for b in sample:
+        L0, nb, ev = int(plan["L0"][b]), int(plan["nb"][b]), int(plan["ev"][b])
+        chunks = [(src[b][0], src[b][1], 0), (kc_b[b: b + 1], vc_b[b: b + 1], L0)]
+        _check_raw_gather_against_oracle(oracle, pool, ntab[b: b + 1], ncl[b: b + 1], DTYPE_INT4, P, Hkv, D, chunks,
+                                         np.arange(ev, nb, dtype=np.int32), int(plan["new_ctx"][b]), pool_blocks=nb)
+    say(f"[c5-full] append + eviction + compaction of sequences {sample.tolist()} byte-exact")
     st = torch.from_numpy(sample).to(gpu)
     kf, vf, _, _ = vr.kv_gather(pool, ntab[st], ncl[st], out_mode=vr.GATHER_F32, max_ctx_len=T)
     kf, vf = kf.cpu().numpy(), vf.cpu().numpy()
@@ -1691,6 +1747,97 @@ def _legacy_append_loop(oracle, D):
         assert np.abs(out - want).max() <= 2e-5, (np.abs(out - want).max(), err)
     finally:
         assert vr.lib().vspec_rocm_release_cache_mirror(C.cast(C.pointer(cache), C.c_void_p)) == 1
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_backend_through_reference_registry(oracle, ref, gpu, mode):
+    """The drop-in through the reference's own registry, compiled from its sources into
+    oracle/_ref (backend_registry.c:3-11): vspec_set_backend stores the ROCm entry by value
+    in the global slot, and vspec_get_backend()->launch_attention, the call
+    vspec_attention_forward makes (runtime.c:641-647), reaches it.  Three contexts: a
+    legacy fp32 VspecKVCache (D = 128 through the paged kernels, D = 20 through the generic
+    one), an int3 cache without its fp32 mirror, and a VSPEC_KCTX_FLAG_PAGED descriptor.
+    The registry path equals the direct call bit for bit; for the two host caches the
+    reference CPU entry (vspec_make_cpu_backend, installed the same way) gives the
+    reference's own result, which the ROCm entry matches within 2e-5 (fp32 rows) and 1e-4
+    (int3 rows)."""
+    import ctypes as C
+    import os
+    import torch
+    import vspec_rocm as vr
+
+    RL = ref.lib
+    RL.vspec_set_backend.argtypes, RL.vspec_set_backend.restype = [vr.VspecBackend], None
+    RL.vspec_get_backend.argtypes, RL.vspec_get_backend.restype = [], C.POINTER(vr.VspecBackend)
+    RL.vspec_make_cpu_backend.argtypes, RL.vspec_make_cpu_backend.restype = [], vr.VspecBackend
+    rocm, cpu = vr.backend(), RL.vspec_make_cpu_backend()
+    if mode:
+        os.environ["VSPEC_3BIT_RUNTIME_MODULE"] = "1"
+    else:
+        os.environ.pop("VSPEC_3BIT_RUNTIME_MODULE", None)
+    os.environ.pop("VSPEC_FUSED_BITS", None)
+
+    def via_registry(entry, kctx):
+        RL.vspec_set_backend(entry)
+        slot = RL.vspec_get_backend().contents
+        assert slot.name == entry.name
+        slot.launch_attention(C.byref(kctx))
+
+    def host_ctx(q, cache):
+        out = np.full((cache.num_heads, cache.head_dim), 7.0, np.float32)
+        kctx = vr.VspecKernelContext()
+        kctx.input, kctx.weight, kctx.output = q.ctypes.data, C.cast(C.pointer(cache), C.c_void_p), out.ctypes.data
+        return kctx, out
+
+    try:
+        for D in (128, 20):
+            H, T = 4, 157
+            k = np.ascontiguousarray(oracle.normal(620 + D, T * H * D).reshape(T, H, D))
+            v = np.ascontiguousarray(oracle.normal(621 + D, T * H * D).reshape(T, H, D))
+            q = np.ascontiguousarray(oracle.normal(622 + D, H * D).reshape(H, D) * 2)
+            k[::11, 1, 3] = 30.0  # keys the std clamp moves
+            for kind in ("fp32", "int3"):
+                if kind == "fp32":
+                    cache = vr.VspecKVCache()
+                    cache.key, cache.value = k.ctypes.data, v.ctypes.data
+                    cache.max_tokens, cache.num_heads, cache.head_dim, cache.current_tokens = T, H, D, T
+                    bufs, tol = (k, v), 2e-5
+                else:
+                    cache, bufs, _, _ = _int3_cache(oracle, k, v, 16, "")
+                    scratch = (np.zeros(D, np.float32), np.zeros(D, np.float32))
+                    cache.scratch_key_head, cache.scratch_value_head = scratch[0].ctypes.data, scratch[1].ctypes.data
+                    tol = 1e-4
+                kc, out_reg = host_ctx(q, cache)
+                via_registry(rocm, kc)
+                err = vr.last_error()
+                kd, out_direct = host_ctx(q, cache)
+                rocm.launch_attention(C.byref(kd))
+                kr, out_cpu = host_ctx(q, cache)
+                via_registry(cpu, kr)
+                assert not np.all(out_reg == 7.0) and not np.all(out_cpu == 7.0), err
+                assert np.array_equal(out_reg.view(np.uint32), out_direct.view(np.uint32)), (D, kind)
+                diff = float(np.abs(out_reg - out_cpu).max())
+                say(f"[registry] mode={mode} D={D} {kind}: rocm vs reference cpu entry max-abs {diff:.2e}")
+                assert diff <= tol, (D, kind, diff)
+                assert vr.lib().vspec_rocm_release_cache_mirror(C.cast(C.pointer(cache), C.c_void_p)) == 1
+        # the paged descriptor (device pointers) through the same slot
+        case = make_case(oracle, DTYPE_F16, 3, 8, 2, 128, 16, [40, 75, 9], seed=45)
+        pool = build_both(oracle, case, gpu)
+        tab = torch.from_numpy(case.tables).to(gpu)
+        ctx_t = torch.from_numpy(case.ctx).to(gpu)
+        qd = torch.from_numpy(case.q).to(gpu)
+        want = vr.paged_decode(pool, tab, ctx_t, qd, numerics=mode)
+        out = torch.zeros_like(qd)
+        d = vr.make_decode_desc(pool, tab, ctx_t, qd, out, case.tmax, numerics=mode)
+        kp = vr.VspecKernelContext()
+        kp.weight = C.cast(C.pointer(d), C.c_void_p)
+        kp.config.flags = vr.KCTX_FLAG_PAGED
+        via_registry(rocm, kp)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        check_attention(oracle, case, out.cpu().numpy(), mode)
+    finally:
+        RL.vspec_set_backend(vr.VspecBackend())
 
 
 def test_backend_int3_cache_rejects_bad_geometry(oracle, gpu):

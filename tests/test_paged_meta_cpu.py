@@ -191,22 +191,25 @@ def _ref_batcher_steps(ref, seed, n_req=6, max_items=8, max_tokens=64, prefill_q
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
-def test_plan_step_follows_reference_scheduler(lib, ref, seed):
+@pytest.mark.parametrize("kept", [False, True])
+def test_plan_step_follows_reference_scheduler(lib, ref, seed, kept):
     """Steps of the reference scheduler planned on the host allocator: the packed token
     map, start positions and context lengths are consistent, and every position of every
     item maps through its block table to the page and slot the reference paged cache
-    (appending the same tokens) holds it in."""
-    from vspec_rocm.sessions import plan_step
+    (appending the same tokens) holds it in.  kept: the tables are kept between steps and
+    only updated (vspec_rocm_paged_plan_step_update)."""
+    from vspec_rocm.sessions import StepPlanner, plan_step
 
     P, MAXP, H, D = 16, 512, 1, 8
     m = lib.vspec_rocm_paged_meta_create(P, MAXP, 0, 0)
     c = ref.lib.vr_paged_new(P, MAXP, H, D)
     tok = np.zeros(H * D, np.float32)
     nsteps = 0
+    planner = StepPlanner(m, max_items=8, max_blocks=64, max_tokens=8 * 64) if kept else None
     try:
         for step in _ref_batcher_steps(ref, seed):
             nsteps += 1
-            plan = plan_step(m, step, max_blocks=64)
+            plan = planner.step(step) if kept else plan_step(m, step, max_blocks=64)
             off = 0
             for i, it in enumerate(step):
                 q = int(it.token_quota)
@@ -296,6 +299,109 @@ def test_plan_step_partial_middle_pages(lib, ref):
     finally:
         lib.vspec_rocm_paged_meta_destroy(m)
         ref.lib.vr_paged_free(c)
+
+
+def _random_steps(rng, n_steps, n_sessions, max_items, max_quota):
+    """Seeded step sequences: items drawn from a small set of sessions in shuffled order
+    (rows change hands between steps), mostly decode quotas of 1 with some prefill chunks,
+    plus prefix reuses into fresh sessions and closes between steps."""
+    next_new = 1000
+    for _ in range(n_steps):
+        ops = []
+        r = rng.random()
+        if r < 0.1:
+            ops.append(("reuse", next_new, int(rng.integers(1, n_sessions + 1)), int(rng.integers(0, 40))))
+            next_new += 1
+        elif r < 0.15:
+            ops.append(("close", int(rng.integers(1, n_sessions + 1))))
+        k = int(rng.integers(1, max_items + 1))
+        ids = rng.choice(np.arange(1, n_sessions + 1), size=k, replace=False).tolist()
+        if ops and ops[0][0] == "reuse" and rng.random() < 0.7:
+            ids[int(rng.integers(0, k))] = ops[0][1]
+        items = []
+        for sid in ids:
+            q = 1 if rng.random() < 0.7 else int(rng.integers(0, max_quota + 1))
+            items.append((int(sid), 2 if q == 1 else 1, q, 0))
+        yield ops, items
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("with_used", [False, True])
+def test_plan_step_update_equals_full_planning(lib, seed, with_used):
+    """Two allocators take the same seeded operations; one plans every step into fresh
+    tables (vspec_rocm_paged_plan_step), the other updates tables it keeps
+    (vspec_rocm_paged_plan_step_update).  Every step gives the same success, block tables,
+    used counts, contexts, start positions and packed-token map, through sessions moving
+    between rows, prefix reuse (shared, partly filled pages), closes, LRU evictions in a
+    small pool, failed steps, and a change of table buffers half way."""
+    from vspec_rocm import VspecRocmError
+    from vspec_rocm.sessions import StepPlanner, plan_step
+
+    rng = np.random.default_rng(300 + seed)
+    P, MAXP, MAXB = 4, int(rng.choice([24, 48, 400])), 32
+    a = lib.vspec_rocm_paged_meta_create(P, MAXP, 16, 0)
+    b = lib.vspec_rocm_paged_meta_create(P, MAXP, 16, 0)
+    planner = StepPlanner(b, max_items=6, max_blocks=MAXB, max_tokens=6 * 9, with_used=with_used)
+    fails = updates = 0
+    try:
+        for n, (ops, items) in enumerate(_random_steps(rng, 300, 10, 6, 9)):
+            if n == 150:  # other buffers: every row is written whole again
+                planner = StepPlanner(b, max_items=6, max_blocks=MAXB, max_tokens=6 * 9, with_used=with_used)
+            for op in ops:
+                if op[0] == "reuse":
+                    ra = lib.vspec_rocm_paged_reuse_prefix(a, op[1], op[2], op[3])
+                    assert ra == lib.vspec_rocm_paged_reuse_prefix(b, op[1], op[2], op[3])
+                else:
+                    assert lib.vspec_rocm_paged_close_session(a, op[1]) == lib.vspec_rocm_paged_close_session(b, op[1])
+            try:
+                want = plan_step(a, items, max_blocks=MAXB, with_used=with_used)
+            except VspecRocmError:
+                want = None
+            try:
+                got = planner.step(items)
+            except VspecRocmError:
+                got = None
+            assert (want is None) == (got is None), n
+            if want is None:
+                fails += 1
+                continue
+            updates += 1
+            for key in want:
+                assert np.array_equal(want[key], got[key]), (n, key)
+            assert _stats(lib, a) == _stats(lib, b)
+        # plain tables refuse every step holding a session with a shared, partly filled
+        # middle page, which prefix reuse keeps creating here
+        assert updates > 50 and (fails < updates or not with_used)
+        if MAXP < 100:
+            assert fails > 0 or _stats(lib, a)[2] > 0  # small pools do evict
+    finally:
+        lib.vspec_rocm_paged_meta_destroy(a)
+        lib.vspec_rocm_paged_meta_destroy(b)
+
+
+def test_plan_step_update_writes_only_changed_entries(lib):
+    """Steady decode over kept tables: after the first step, a step of one token per
+    sequence changes only the entries it must (the last entry's used count, a new page
+    every P tokens).  Entries outside them are left untouched, which the test checks by
+    planting a marker the planner must not overwrite."""
+    from vspec_rocm.sessions import StepPlanner
+
+    P, B = 16, 8
+    m = lib.vspec_rocm_paged_meta_create(P, 4096, 0, 0)
+    planner = StepPlanner(m, max_items=B, max_blocks=64, max_tokens=B * 100, with_used=True)
+    try:
+        planner.step([(i + 1, 1, 100, 0) for i in range(B)])  # prefill 100 tokens each
+        for t in range(40):
+            n_pages = (100 + t) // P  # entries before the current last one
+            planner.used[:, : n_pages - 1] = -7   # planted: full pages the update must not touch
+            plan = planner.step([(i + 1, 2, 1, 0) for i in range(B)])
+            assert (plan["block_used"][:, : n_pages - 1] == -7).all(), t
+            assert (plan["ctx_lens"] == 101 + t).all()
+            last = (100 + t) // P
+            assert (plan["block_used"][:, last] == (100 + t) % P + 1).all()
+            planner.used[:, : n_pages - 1] = P
+    finally:
+        lib.vspec_rocm_paged_meta_destroy(m)
 
 
 def test_plan_step_rejects_bad_steps(lib):

@@ -192,6 +192,9 @@ SIGNATURES = {
     "vspec_rocm_kv_gather_rows": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, _vp, _vp]),
     "vspec_rocm_paged_plan_step": (C.c_int, [_vp, C.POINTER(VspecRocmStepItem), C.c_size_t, _i32p_, _i32p_, C.c_size_t,
                                              _i32p_, _i32p_, _i32p_, _i32p_, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "vspec_rocm_paged_plan_step_update": (C.c_int, [_vp, C.POINTER(VspecRocmStepItem), C.c_size_t, _i32p_, _i32p_,
+                                                    C.c_size_t, _i32p_, _i32p_, _i32p_, _i32p_, C.c_size_t,
+                                                    C.POINTER(C.c_size_t)]),
     "vspec_rocm_kv_append_tokens": (C.c_int, [C.POINTER(VspecPagedKV), C.c_uint32, _vp, _vp, _vp, C.c_uint32,
                                               C.c_uint32, _vp, _vp, C.c_int32, _vp]),
     "vspec_rocm_release_retired_workspaces": (C.c_int, []),

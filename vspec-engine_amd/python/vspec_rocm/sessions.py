@@ -190,3 +190,45 @@ def plan_step(meta, items, max_blocks: int, max_tokens: int | None = None, with_
     if with_used:
         out["block_used"] = used[:n]
     return out
+
+
+class StepPlanner:
+    """vspec_rocm_paged_plan_step_update over host tables kept between steps.
+
+    The planner owns block_tables [max_items][max_blocks] (and block_used with with_used),
+    ctx_lens, start_pos and the packed-token map; each step() updates only the row entries
+    that changed since the previous step and returns views of the first n rows, with the
+    same keys as plan_step().  The views are overwritten by the next step."""
+
+    def __init__(self, meta, max_items: int, max_blocks: int, max_tokens: int, with_used: bool = False):
+        self.meta, self.max_items, self.max_blocks, self.max_tokens = meta, max_items, max_blocks, max_tokens
+        self.tables = np.full((max(max_items, 1), max_blocks), -1, np.int32)
+        self.used = np.zeros((max(max_items, 1), max_blocks), np.int32) if with_used else None
+        self.ctx = np.zeros(max(max_items, 1), np.int32)
+        self.start = np.zeros(max(max_items, 1), np.int32)
+        self.titem = np.zeros(max(max_tokens, 1), np.int32)
+        self.tpos = np.zeros(max(max_tokens, 1), np.int32)
+        self._items = (VspecRocmStepItem * max(max_items, 1))()
+        p32 = lambda a: None if a is None else a.ctypes.data_as(C.POINTER(C.c_int32))
+        self._p = [p32(a) for a in (self.tables, self.used, self.ctx, self.start, self.titem, self.tpos)]
+        self._got = C.c_size_t()
+
+    def step(self, items):
+        n = len(items)
+        if n > self.max_items:
+            raise VspecRocmError(f"step of {n} items exceeds the planner's {self.max_items}")
+        for i, it in enumerate(items):
+            self._items[i] = it if isinstance(it, VspecRocmStepItem) else VspecRocmStepItem(*[int(x) for x in it])
+        pt, pu, pc, ps, pi, pp = self._p
+        ok = lib().vspec_rocm_paged_plan_step_update(self.meta, self._items, n, pt, pu, self.max_blocks, pc, ps, pi,
+                                                     pp, self.max_tokens, C.byref(self._got))
+        if not ok:
+            raise VspecRocmError("plan_step_update failed (pool exhausted, eviction of a batch member, repeated "
+                                 "request, shared partly filled page, or outputs too small)")
+        t = int(self._got.value)
+        out = dict(block_tables=self.tables[:n], ctx_lens=self.ctx[:n], start_pos=self.start[:n],
+                   token_item=self.titem[:t], token_pos=self.tpos[:t])
+        if self.used is not None:
+            out["block_used"] = self.used[:n]
+        return out
+
