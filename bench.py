@@ -403,7 +403,7 @@ def run_legacy(args):
     T, H, D = args.legacy_tokens, 8, 128
     steps = max(args.steps, 10)
     rng = np.random.default_rng(args.seed)
-    cap = T + steps + args.warmup + max(5, steps // 10) + 2
+    cap = T + args.warmup + steps + 2 * max(5, steps // 10) + 2
     kb = rng.standard_normal((cap, H, D)).astype(np.float32)
     vb = rng.standard_normal((cap, H, D)).astype(np.float32)
     q = rng.standard_normal((H, D)).astype(np.float32)
