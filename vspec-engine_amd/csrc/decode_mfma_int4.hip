@@ -903,11 +903,12 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
                     if (live) {
                         fetch_k(stg[u][wave], 0, fa);
                         fetch_k(stg[u][wave], 1, fb);
+                        // raw V scale bits of the pair: lanes 0-31 tile a, 32-63 tile b (read
+                        // ahead of the scores, which hide its latency)
+                        vsw = (lane & 31) < 8 * NG ? stg[u][wave].sc[lane >> 5][32 + (lane & 31)] : 0u;
                         scores(qn, fa, fb, nva, nvb, t, pr);
                         fetch_v(stg[u][wave], 0, fa);
                         fetch_v(stg[u][wave], 1, fb);
-                        // raw V scale bits of the pair: lanes 0-31 tile a, 32-63 tile b
-                        vsw = (lane & 31) < 8 * NG ? stg[u][wave].sc[lane >> 5][32 + (lane & 31)] : 0u;
                     }
                     // the stage is read: reload it with the pair ST steps ahead
                     wait_lds_reads();
