@@ -538,7 +538,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the paged decode "
-              "path shards by sequence or kv head with no exchange; see DESIGN.md). Run with --gpus 1.",
+              "path would shard by sequence or kv head, with no exchange between GPUs). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
