@@ -20,7 +20,6 @@
 // The std clamp is screened per key from v_dot2 sums (sum x, sum x^2) and a packed
 // max|x|; keys it may affect (about 0.1% for N(0,1) data) get their scores recomputed
 // exactly in fp32 from the clipped row, replacing the MFMA value.
-#include "append_row.h"
 #include "kv_common.h"
 
 namespace vkv {
@@ -39,113 +38,6 @@ struct Frags {
     uint4 k[D / 32];  // K row of token n, d = 32i + 8g .. +7
     uint2 v[D / 16];  // V^T row d = 16j + n, slots 4g .. 4g+3 of the tile
 };
-
-// Fused decode-step append for f16 pools, run by one wave: the token rows of every work
-// item whose last tile lies in the range [ws.lo, ws.hi) (c: the item holding ws.lo), which
-// exactly one workgroup covers.  Lanes take (item, 8-element chunk of K or V) pairs, IPP
-// items per pass and PASSES passes per round, and all loads of a round go out before its
-// stores: the items' contexts and source chunks together, then their table entries.  The
-// bytes written are those of append_chunk<VSPEC_KV_F16> (a copy of f16 source bits, or the
-// round-to-nearest-even conversion of f32 ones), so a range with many short items costs a
-// few load round trips instead of one chain of dependent loads and stores per item.
-template <int D>
-__device__ void fused_append_f16(const DecodeParams& p, const WorkSplit& ws, ItemCursor c, const int ips,
-                                 const int lane) {
-    constexpr int CH = D / 8;       // 8-element chunks per row
-    constexpr int LPI = 2 * CH;     // lanes per item: K chunks, then V chunks
-    constexpr int IPP = 64 / LPI;   // items per pass
-    constexpr int PASSES = 8;
-    static_assert(64 % LPI == 0, "items per pass");
-    const int chunk = (lane % LPI) % CH;
-    const int which = (lane % LPI) / CH;  // 0: K, 1: V
-    const int my = lane / LPI;            // this lane's item slot in a pass
-    const bool f32src = p.append_src == VSPEC_KV_F32;
-    bool done = false;
-    while (!done) {
-        int ib[PASSES], ih[PASSES];  // per pass: this lane's sequence (-1: none) and kv head
-#pragma unroll
-        for (int k = 0; k < PASSES; ++k) {
-            ib[k] = -1;
-            ih[k] = 0;
-#pragma unroll
-            for (int i = 0; i < IPP; ++i) {
-                int fb = -1, fh = 0;
-                while (!done) {
-                    const int last = c.item0 + c.U - 1;
-                    const bool mine = last >= ws.lo && last < ws.hi;
-                    const int cb = c.b, chk = c.y / (int)p.gsplit;
-                    if (c.item0 + c.U >= ws.hi) done = true;
-                    else cursor_next(p, ips, c);
-                    if (mine) {
-                        fb = cb;
-                        fh = chk;
-                        break;
-                    }
-                }
-                if (my == i) {
-                    ib[k] = fb;
-                    ih[k] = fh;
-                }
-            }
-        }
-        int ctx[PASSES];
-        uint4 s0[PASSES], s1[PASSES];
-#pragma unroll
-        for (int k = 0; k < PASSES; ++k) {
-            ctx[k] = 0;
-            if (ib[k] >= 0) {
-                ctx[k] = p.ctx_lens[ib[k]];
-                const size_t el = ((size_t)ib[k] * p.hkv + ih[k]) * D + (size_t)chunk * 8;
-                const uint8_t* src = which ? p.v_new : p.k_new;
-                if (f32src) {
-                    s0[k] = *reinterpret_cast<const uint4*>(src + el * 4);
-                    s1[k] = *reinterpret_cast<const uint4*>(src + el * 4 + 16);
-                } else {
-                    s0[k] = *reinterpret_cast<const uint4*>(src + el * 2);
-                }
-            }
-        }
-        int ent[PASSES];
-#pragma unroll
-        for (int k = 0; k < PASSES; ++k) {
-            ent[k] = -1;
-            if (ib[k] >= 0 && ctx[k] > 0) {
-                const uint32_t lb = (uint32_t)(ctx[k] - 1) / p.block_tokens;
-                if (lb < p.max_blocks) ent[k] = p.block_tables[(size_t)ib[k] * p.max_blocks + lb];
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < PASSES; ++k) {
-            if (ent[k] < 0 || (uint32_t)ent[k] >= p.num_blocks) continue;
-            const uint32_t slot = (uint32_t)(ctx[k] - 1) % p.block_tokens;
-            const size_t bh = (size_t)ent[k] * p.hkv + ih[k];
-            uint32_t hb[8];
-            if (f32src) {
-                const float xs[8] = {__uint_as_float(s0[k].x), __uint_as_float(s0[k].y), __uint_as_float(s0[k].z),
-                                     __uint_as_float(s0[k].w), __uint_as_float(s1[k].x), __uint_as_float(s1[k].y),
-                                     __uint_as_float(s1[k].z), __uint_as_float(s1[k].w)};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) hb[e] = float_to_half_bits(xs[e]);
-            } else {
-                const uint32_t ws4[4] = {s0[k].x, s0[k].y, s0[k].z, s0[k].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    hb[2 * e] = ws4[e] & 0xffffu;
-                    hb[2 * e + 1] = ws4[e] >> 16;
-                }
-            }
-            if (which) {
-                // V tiles are d-major: element (d, slot) at tile + d*P + slot
-                uint16_t* vt = reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(p.v)) + bh * D * p.block_tokens + slot;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) vt[(size_t)(chunk * 8 + e) * p.block_tokens] = (uint16_t)hb[e];
-            } else {
-                *reinterpret_cast<uint4*>(const_cast<uint8_t*>(p.k) + ((bh * p.block_tokens + slot) * D + chunk * 8) * 2) =
-                    make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16), hb[6] | (hb[7] << 16));
-            }
-        }
-    }
-}
 
 // PB: block_tokens known at compile time (16), or 0 for any multiple of 16;
 // NB: tiles in flight per wave; USED: per-block used counts cap each tile (block_used)
@@ -172,6 +64,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
     __shared__ int patch_flag[NW][kTile];
     __shared__ int slot_cnt[kSlots];
     __shared__ int slot_seg[kSlots];
+    // fused decode step: the new token's K and V rows (f16 bits, two per word) of segment s
+    // in row s < kQStage (staged up front), of a later segment in row kQStage + wave (staged
+    // by the wave itself); the wave that processes the tile holding the token patches them
+    // into its fragments and stores them to the pool, so no wave waits for those stores
+    __shared__ uint32_t newtok[kQStage + NW][2][D / 2];
     __shared__ SplitSharedN<NW> split_sh;
 
     const int lane = threadIdx.x & 63;
@@ -200,6 +97,36 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
     // score clip per lane: columns that hold no head clip to -inf (3-bit mode: +-24*log2e)
     const float clip_hi = n < GW ? p.logit_clip : -INFINITY;
     const float clip_lo = n < GW ? -p.logit_clip : -INFINITY;
+    // The new token rows of item c into newtok[row] (one wave; lane l takes elements 2l,
+    // 2l + 1 of K and of V).  The bits are those the pool append writes (f16 source bits, or
+    // the round-to-nearest-even conversion of f32 ones).  load() issues the loads, store()
+    // writes LDS once they have landed.
+    struct NewRow {
+        uint32_t kw, vw;
+        float2 kf, vf;
+    };
+    auto newrow_load = [&](const ItemCursor& c) -> NewRow {
+        NewRow r = {0u, 0u, make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
+        const size_t el = ((size_t)c.b * p.hkv + c.y / (int)p.gsplit) * D + 2 * lane;
+        if (p.append_src == VSPEC_KV_F32) {
+            r.kf = *reinterpret_cast<const float2*>(p.k_new + el * 4);
+            r.vf = *reinterpret_cast<const float2*>(p.v_new + el * 4);
+        } else {
+            r.kw = *reinterpret_cast<const uint32_t*>(p.k_new + el * 2);
+            r.vw = *reinterpret_cast<const uint32_t*>(p.v_new + el * 2);
+        }
+        return r;
+    };
+    auto newrow_store = [&](const NewRow& r, const int row) {
+        uint32_t kw = r.kw, vw = r.vw;
+        if (p.append_src == VSPEC_KV_F32) {
+            kw = float_to_half_bits(r.kf.x) | (float_to_half_bits(r.kf.y) << 16);
+            vw = float_to_half_bits(r.vf.x) | (float_to_half_bits(r.vf.y) << 16);
+        }
+        newtok[row][0][lane] = kw;
+        newtok[row][1][lane] = vw;
+    };
+
     auto qprep = [&](const int s, const ItemCursor& c) {
         constexpr int E = D / 64;
         if (s >= kQStage) {
@@ -212,6 +139,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
 #pragma unroll
                 for (int e = 0; e < E; ++e) qs[wave][h][lane * E + e] = qrow[lane * E + e];
             }
+            if (p.k_new) newrow_store(newrow_load(c), kQStage + wave);
         }
         float (*src)[D] = s < kQStage ? qraw[s] : qs[wave];
         int eh[GW];
@@ -513,6 +441,68 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
         }
     };
 
+    // The staged new token (segment s, slot ts of the tile) into a tile's fragments: lanes
+    // n == ts hold its K row, lanes g == ts / 4 its V column (element ts % 4 of each pack).
+    auto patch_new = [&](Frags<D>& f, const int s, const int ts) {
+        const int row = s < kQStage ? s : kQStage + wave;
+        if (n == ts) {
+#pragma unroll
+            for (int i = 0; i < NQK; ++i) {
+                const uint32_t* kw = &newtok[row][0][16 * i + 4 * g];
+                f.k[i] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+            }
+        }
+        if (g == ts / 4) {
+#pragma unroll
+            for (int j = 0; j < NDT; ++j) {
+                const int d = 16 * j + n;
+                const uint16_t h = (uint16_t)(newtok[row][1][d / 2] >> (16 * (d & 1)));
+                uint16_t e[4];
+                e[0] = (uint16_t)f.v[j].x;
+                e[1] = (uint16_t)(f.v[j].x >> 16);
+                e[2] = (uint16_t)f.v[j].y;
+                e[3] = (uint16_t)(f.v[j].y >> 16);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) e[r] = r == ts % 4 ? h : e[r];
+                f.v[j] = make_uint2(e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16));
+            }
+        }
+    };
+
+    // The staged new token of item c (segment s, position pos) into the pool, by the wave
+    // that processes the item's tile holding it (or, for a token past the decoded tiles,
+    // the item's last decoded tile): the lanes that hold its K row and V column store them
+    // from LDS, with no wait.  Nothing in this launch reads these bytes back from the pool:
+    // every reader of the tile patches the token in from LDS.  The bytes are those of
+    // append_chunk<VSPEC_KV_F16>; a position past the table or an invalid block writes
+    // nothing.
+    auto store_new = [&](const ItemCursor& c, const int s, const int pos) {
+        const int row = s < kQStage ? s : kQStage + wave;
+        const uint32_t lb = (uint32_t)pos / p.block_tokens;
+        if (lb >= p.max_blocks) return;
+        const int entry = as_const(p.block_tables)[(size_t)c.b * p.max_blocks + lb];
+        if (entry < 0 || (uint32_t)entry >= p.num_blocks) return;
+        const uint32_t slot = (uint32_t)pos % p.block_tokens;
+        const size_t bh = (size_t)entry * p.hkv + c.y / (int)p.gsplit;
+        const int ts = pos % kTile;
+        if (n == ts) {
+            uint4* kd = reinterpret_cast<uint4*>(const_cast<uint8_t*>(p.k) + ((bh * p.block_tokens + slot) * D) * 2);
+#pragma unroll
+            for (int i = 0; i < NQK; ++i) {
+                const uint32_t* kw = &newtok[row][0][16 * i + 4 * g];
+                kd[4 * i + g] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+            }
+        }
+        if (g == ts / 4) {
+            uint16_t* vd = reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(p.v)) + bh * D * p.block_tokens + slot;
+#pragma unroll
+            for (int j = 0; j < NDT; ++j) {
+                const int d = 16 * j + n;
+                vd[(size_t)d * p.block_tokens] = (uint16_t)(newtok[row][1][d / 2] >> (16 * (d & 1)));
+            }
+        }
+    };
+
     // NB tiles in flight per wave: buffer u holds the wave's tile k + u and is reloaded
     // with the tile NB steps ahead right after it is processed.  The trip count is
     // uniform per wave (rounded up to NB; the extra tiles are out of range and fully
@@ -520,33 +510,28 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
     // wait counts stay exact.
     ItemCursor pc = first;  // work item of the tiles being processed
     int seg = 0;            // its segment index in this workgroup
+    // position of the item's new token (fused decode step), -1: none or outside the table
+    auto new_pos = [&](const int b) -> int {
+        const int c = as_const(p.ctx_lens)[b];
+        return p.k_new && c >= 1 && c <= ctx_cap ? c - 1 : -1;
+    };
     int pctx = min(max(as_const(p.ctx_lens)[pc.b], 0), ctx_cap);
+    int papp = new_pos(pc.b);
     const int len = ws.hi - ws.lo;
     const int t0 = ws.lo + wave;
     const int nt = wave < len ? (len - wave + NW - 1) / NW : 0;
     Frags<D> f[NB];
     int ok[NB];
     // Set-up.  Wave 0 loads the q rows of the range's first kQStage segments (rows GW*y ..
-    // GW*y + GW - 1 of sequence b are contiguous; merge slot s serves segment s first) and
-    // writes the fused append's token rows, waits for both (nothing else of it is in
-    // flight, so the wait is short), stages the q rows in LDS, then issues its first NB
-    // tiles.  Waves 1.. issue their first NB tiles at once.  The barrier (an LDS-only wait:
-    // the other waves' tile loads stay in flight) publishes the q rows and the appended
-    // rows, and every wave prepares its q operands while its tiles are on the way.  A wave
-    // whose first NB tiles include a tile this workgroup appends into (the last tile of
-    // an item ending in the range) issues them after the barrier.
+    // GW*y + GW - 1 of sequence b are contiguous; merge slot s serves segment s first) and,
+    // for a fused decode step, their new token rows, waits for these loads only, stages
+    // both in LDS, then issues its first NB tiles.  Waves 1.. issue their first NB tiles at
+    // once.  The barrier (an LDS-only wait: the other waves' tile loads stay in flight)
+    // publishes the staged rows, and every wave prepares its q operands while its tiles are
+    // on the way.  The tile holding an item's new token may be read from the pool before
+    // the token is stored there: the wave that processes it patches the token's K row and V
+    // column in from LDS and then issues the token's pool stores.
     constexpr int QPL = (GW * D + 63) / 64;  // q floats per lane of wave 0 and segment
-    bool defer = false;
-    if (p.k_new && wave != 0) {
-        ItemCursor c = first;
-        const int end = min(ws.hi, ws.lo + NB * NW);
-        while (true) {
-            const int last = c.item0 + c.U - 1;
-            if (last >= ws.lo && last < end && (last - ws.lo) % NW == wave) defer = true;
-            if (c.item0 + c.U >= end) break;
-            cursor_next(p, ips, c);
-        }
-    }
     if (wave == 0) {
         int nseg = 1;
         {
@@ -557,6 +542,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
             }
         }
         float qreg[kQStage][QPL];
+        NewRow nrow[kQStage];
         {
             ItemCursor c = first;
 #pragma unroll
@@ -568,12 +554,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
                         const int i = lane + 64 * j;
                         qreg[s][j] = i < GW * D ? qrow[i] : 0.f;
                     }
+                    if (p.k_new) nrow[s] = newrow_load(c);
                     if (s + 1 < nseg) cursor_next(p, ips, c);
                 }
             }
         }
-        if (p.k_new) fused_append_f16<D>(p, ws, first, ips, lane);
-        __builtin_amdgcn_s_waitcnt(0);  // q rows loaded, appended rows stored
+        __builtin_amdgcn_s_waitcnt(0);  // q rows and new token rows loaded
 #pragma unroll
         for (int s = 0; s < kQStage; ++s) {
             if (s < nseg) {
@@ -582,6 +568,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
                     const int i = lane + 64 * j;
                     if (i < GW * D) qraw[s][i / D][i % D] = qreg[s][j];
                 }
+                if (p.k_new) newrow_store(nrow[s], s);
             }
         }
         if (lane < kSlots) {
@@ -589,15 +576,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
             slot_seg[lane] = lane;
         }
     }
-    if (!defer) {
 #pragma unroll
-        for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * NW, f[u]);
-    }
+    for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * NW, f[u]);
     __syncthreads();
-    if (defer) {
-#pragma unroll
-        for (int u = 0; u < NB; ++u) ok[u] = load(t0 + u * NW, f[u]);
-    }
     reset();
     qprep(0, pc);
     for (int k = 0; k < nt; k += NB) {
@@ -612,7 +593,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
                     reset();
                 } while (t >= pc.item0 + pc.U);
                 pctx = min(max(as_const(p.ctx_lens)[pc.b], 0), ctx_cap);
+                papp = new_pos(pc.b);
                 qprep(seg, pc);
+            }
+            if (papp >= 0 && t - pc.item0 == min(papp / kTile, pc.U - 1)) {
+                if (t - pc.item0 == papp / kTile) patch_new(f[u], seg, papp % kTile);
+                store_new(pc, seg, papp);
             }
             process(f[u], ok[u], t - pc.item0, pctx);
             ok[u] = load(t + NB * NW, f[u]);
