@@ -596,7 +596,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
                 papp = new_pos(pc.b);
                 qprep(seg, pc);
             }
-            if (papp >= 0 && t - pc.item0 == min(papp / kTile, pc.U - 1)) {
+            // (a tile past the range belongs to another workgroup, which stores the token)
+            if (papp >= 0 && t < ws.hi && t - pc.item0 == min(papp / kTile, pc.U - 1)) {
                 if (t - pc.item0 == papp / kTile) patch_new(f[u], seg, papp % kTile);
                 store_new(pc, seg, papp);
             }
