@@ -12,8 +12,10 @@
  *
  * HBM layout (decision D6), element (block b, kv head h, slot s, dim d):
  *   K, and V of f32 pools  data[((b*H + h)*P + s)*D + d]          (token-major rows)
- *   V of f16 pools         data[((b*H + h)*D + d)*P + s]          (d-major: the matrix-core
- *                          operand of P.V needs consecutive tokens of one d per lane)
+ *   V of f16 pools         data[(b*H + h)*D*P + (s/4)*4*D + 4*d + s%4]  (groups of 4 tokens,
+ *                          d-major inside a group: the matrix-core operand of P.V needs 4
+ *                          consecutive tokens of one d per lane, and one token's row then
+ *                          spans 4*D halves instead of D*P)
  *   int4 pools (K and V)   codes byte ((b*H + h)*P + s)*(D/2) + d/2, nibble d&1 (even = low);
  *                          scale  ((b*H + h)*P + s)*(D/32) + d/32, fp16 bits
  * so one (block, head) tile of P tokens is contiguous (4 KB at P=16, D=128, f16).

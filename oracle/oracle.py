@@ -129,6 +129,7 @@ class Oracle:
                                                _vp, _vp, C.c_int, _f32p, _f32p, _sz, _sz]),
             "vo_int4_ks_index": (_sz, [C.POINTER(VoPagedKV), _sz, _sz, _sz, _sz]),
             "vo_int4_v_byte": (_sz, [C.POINTER(VoPagedKV), _sz, _sz, _sz, _sz, C.POINTER(C.c_int)]),
+            "vo_f16_v_index": (_sz, [C.POINTER(VoPagedKV), _sz, _sz, _sz, _sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

@@ -594,6 +594,7 @@ static int vo_kv_valid(const VoPagedKV* kv) {
                            kv->block_tokens % 16u != 0u || !kv->k_scales || !kv->v_scales)) {
         return 0;
     }
+    if (kv->dtype == 1 && kv->block_tokens % 16u != 0u) return 0; /* f16 V in 16-token tiles */
     return 1;
 }
 
@@ -607,7 +608,8 @@ static long vo_phys_block(const VoPagedKV* kv, const int32_t* block_tables, uint
     return (long)pb;
 }
 
-/* f16 V tiles are d-major: element (d, slot) of tile (b, h) at ((b*H + h)*D + d)*P + slot.
+/* f16 V: per (block b, head h), groups of 4 tokens; element (d, slot) at
+ *   (b*H + h)*D*P + (slot/4)*4*D + 4*d + slot%4      (vo_f16_v_index; P a multiple of 16)
  * int4 pools (block_tokens a multiple of 16):
  *   K codes: token-major rows of D/2 bytes, element e in nibble e%2 of byte e/2;
  *   K scales: group-major, scale (group c, slot) at ((b*H + h)*G + c)*P + slot;
@@ -616,7 +618,12 @@ static long vo_phys_block(const VoPagedKV* kv, const int32_t* block_tables, uint
  *            of its tile, low nibble when (d/16) is even, high nibble otherwise;
  *   V scales: token-major rows of G scales.
  * Every other array is token-major (row index (b*H + h)*P + slot). */
-static int vo_v_dmajor(const VoPagedKV* kv, int is_v) { return is_v && kv->dtype == 1; }
+static int vo_v_grouped(const VoPagedKV* kv, int is_v) { return is_v && kv->dtype == 1; }
+
+size_t vo_f16_v_index(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t d) {
+    const size_t D = kv->head_dim, P = kv->block_tokens;
+    return (b * kv->num_kv_heads + h) * D * P + (slot / 4u) * 4u * D + 4u * d + slot % 4u;
+}
 
 size_t vo_int4_ks_index(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t group) {
     const size_t G = kv->head_dim / 32u;
@@ -674,13 +681,13 @@ static void vo_int4_get_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, s
 /* Write one token-head row (D elements) from fp32 values into the pool. */
 static void vo_store_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
                          const float* src) {
-    const size_t D = kv->head_dim, P = kv->block_tokens;
+    const size_t D = kv->head_dim;
     void* data = is_v ? kv->v_data : kv->k_data;
     uint16_t* scales = is_v ? kv->v_scales : kv->k_scales;
     const size_t row = vo_row_index(kv, b, h, slot);
-    if (vo_v_dmajor(kv, is_v)) {
-        uint16_t* t = (uint16_t*)data + (b * kv->num_kv_heads + h) * D * P + slot;
-        for (size_t d = 0; d < D; ++d) t[d * P] = vo_float_to_half(src[d]);
+    if (vo_v_grouped(kv, is_v)) {
+        uint16_t* t = (uint16_t*)data;
+        for (size_t d = 0; d < D; ++d) t[vo_f16_v_index(kv, b, h, slot, d)] = vo_float_to_half(src[d]);
     } else if (kv->dtype == 0) {
         memcpy((float*)data + row * D, src, D * sizeof(float));
     } else if (kv->dtype == 1) {
@@ -698,13 +705,13 @@ static void vo_store_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size
 /* Read one token-head row from the pool as fp32 (exact for all three formats). */
 static void vo_load_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
                         float* dst) {
-    const size_t D = kv->head_dim, P = kv->block_tokens;
+    const size_t D = kv->head_dim;
     const void* data = is_v ? kv->v_data : kv->k_data;
     const uint16_t* scales = is_v ? kv->v_scales : kv->k_scales;
     const size_t row = vo_row_index(kv, b, h, slot);
-    if (vo_v_dmajor(kv, is_v)) {
-        const uint16_t* t = (const uint16_t*)data + (b * kv->num_kv_heads + h) * D * P + slot;
-        for (size_t d = 0; d < D; ++d) dst[d] = vo_half_to_float(t[d * P]);
+    if (vo_v_grouped(kv, is_v)) {
+        const uint16_t* t = (const uint16_t*)data;
+        for (size_t d = 0; d < D; ++d) dst[d] = vo_half_to_float(t[vo_f16_v_index(kv, b, h, slot, d)]);
     } else if (kv->dtype == 0) {
         memcpy(dst, (const float*)data + row * D, D * sizeof(float));
     } else if (kv->dtype == 1) {
@@ -722,13 +729,13 @@ static void vo_load_row(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_
 /* Raw (pool-format) copy of one token-head row into a token-major output row. */
 static void vo_copy_row_raw(const VoPagedKV* kv, int is_v, size_t b, size_t h, size_t slot,
                             void* out_row, uint16_t* out_scales) {
-    const size_t D = kv->head_dim, P = kv->block_tokens, G = D / 32u;
+    const size_t D = kv->head_dim, G = D / 32u;
     const void* data = is_v ? kv->v_data : kv->k_data;
     const uint16_t* scales = is_v ? kv->v_scales : kv->k_scales;
     const size_t row = vo_row_index(kv, b, h, slot);
-    if (vo_v_dmajor(kv, is_v)) {
-        const uint16_t* t = (const uint16_t*)data + (b * kv->num_kv_heads + h) * D * P + slot;
-        for (size_t d = 0; d < D; ++d) ((uint16_t*)out_row)[d] = t[d * P];
+    if (vo_v_grouped(kv, is_v)) {
+        const uint16_t* t = (const uint16_t*)data;
+        for (size_t d = 0; d < D; ++d) ((uint16_t*)out_row)[d] = t[vo_f16_v_index(kv, b, h, slot, d)];
     } else if (kv->dtype == 0) {
         memcpy(out_row, (const float*)data + row * D, D * 4u);
     } else if (kv->dtype == 1) {

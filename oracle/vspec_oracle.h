@@ -114,6 +114,11 @@ typedef struct VoPagedKV {
 size_t vo_int4_ks_index(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t group);
 size_t vo_int4_v_byte(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t d, int* high);
 
+/* f16 pool addressing (block_tokens a multiple of 16): index (in halves) of V element
+ * (slot, d) of block b, head h in v_data: groups of 4 tokens, d-major inside a group.
+ * K is token-major. */
+size_t vo_f16_v_index(const VoPagedKV* kv, size_t b, size_t h, size_t slot, size_t d);
+
 /* Append n_new tokens per sequence at logical positions start_pos[b] .. +n_new-1.
  * k_new/v_new: [B][n_new][H][D] in src_dtype (0 f32, 1 f16).  Returns 1/0. */
 int vo_paged_append(const VoPagedKV* kv, uint32_t batch, const int32_t* block_tables,

@@ -349,6 +349,38 @@ def test_int4_pool_layout_is_a_bijection(oracle, D):
     assert hi.value == 1 and at1 == at0
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_f16_v_layout_is_a_bijection(oracle, D):
+    """Every (block, head, slot, element) of an f16 V pool owns exactly one half inside the
+    pool; a 16-token tile is one contiguous span of 16*D halves; the 4 tokens of a group
+    are adjacent for every d (the decode's 8-byte operand); one token's row lies inside
+    its group's 4*D halves, every 4th one."""
+    nb, P, H = 3, 32, 2
+    pool = HostPool(DTYPE_F16, nb, P, H, D)
+    desc = pool.desc()
+    seen = np.full(pool.v.size, -1, np.int64)
+    for b in range(nb):
+        for h in range(H):
+            for slot in range(P):
+                at = [oracle.lib.vo_f16_v_index(C.byref(desc), b, h, slot, d) for d in range(D)]
+                assert max(at) < pool.v.size and (seen[at] < 0).all()
+                seen[at] = (b * H + h) * P + slot
+                g0 = ((b * H + h) * P + slot // 4 * 4) * D
+                assert at == [g0 + 4 * d + slot % 4 for d in range(D)]
+    assert (seen >= 0).all()
+    for b, h, t in ((0, 0, 0), (2, 1, 1)):
+        span = sorted(oracle.lib.vo_f16_v_index(C.byref(desc), b, h, 16 * t + s, d) for s in range(16) for d in range(D))
+        assert span == list(range(span[0], span[0] + 16 * D))
+        quad = [oracle.lib.vo_f16_v_index(C.byref(desc), b, h, 16 * t + 4 + r, 7) for r in range(4)]
+        assert quad == list(range(quad[0], quad[0] + 4))
+
+
+def test_f16_pool_needs_whole_tiles(oracle):
+    pool = HostPool(DTYPE_F16, 2, 24, 1, 64)
+    x = np.zeros((1, 1, 1, 64), np.float32)
+    assert not oracle.paged_append(pool, np.array([[0, 1]], np.int32), np.zeros(1, np.int32), x, x)
+
+
 def test_int4_pool_needs_whole_tiles(oracle):
     pool = HostPool(DTYPE_INT4, 2, 24, 1, 64)
     x = np.zeros((1, 1, 1, 64), np.float32)

@@ -229,11 +229,11 @@ __device__ __forceinline__ void append_chunk(const AppendParams& p, uint32_t seq
             for (int k = 0; k < 8; ++k) hb[k] = float_to_half_bits(x[k]);
         }
         if (which) {
-            // V tiles are d-major: element (d, slot) at tile + d*P + slot
+            // V in 4-token groups: element (d, slot) at f16_v_index (stride 4 in d)
             uint16_t* vt = reinterpret_cast<uint16_t*>(dst) +
-                           ((size_t)phys * p.hkv + h) * p.head_dim * p.block_tokens + slot;
+                           f16_v_index((size_t)phys * p.hkv + h, p.block_tokens, p.head_dim, slot, e0);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) vt[(e0 + k) * p.block_tokens] = (uint16_t)hb[k];
+            for (int k = 0; k < 8; ++k) vt[4 * k] = (uint16_t)hb[k];
         } else {
             *reinterpret_cast<uint4*>(dst + (row * p.head_dim + e0) * 2) =
                 make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16),

@@ -7,7 +7,8 @@
 //                                                   loaded, B = q' split in fp16 hi + lo
 //                                                   (separate accumulator chains)
 //   O^T[d][16 col]     += V^T[d][16 tok] x P^T     v_mfma_f32_16x16x16f16, A = V^T rows
-//                                                   (V is stored d-major per block), B = p
+//                                                   (V is stored in groups of 4 tokens,
+//                                                   f16_v_index), B = p
 //                                                   hi + lo taken straight from the S^T
 //                                                   accumulator registers
 // Columns 0..GW-1 are the GQA query heads that share the tile; the rest stay zero.
@@ -221,9 +222,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
         const uint4* kr = reinterpret_cast<const uint4*>(kbase + (tidx * P + slot0 + n) * D + 8 * g);
 #pragma unroll
         for (int i = 0; i < NQK; ++i) f.k[i] = load_stream4(kr + 4 * i);
-        const _Float16* vt = vbase + tidx * (size_t)D * P + slot0 + 4 * g;
+        // tokens slot0 + 4g .. + 3 of d = 16j + n: 8 bytes at f16_v_index (one 512-byte span per j)
+        const _Float16* vt = vbase + f16_v_index(tidx, P, D, slot0 + 4 * g, n);
 #pragma unroll
-        for (int j = 0; j < NDT; ++j) f.v[j] = load_stream2(vt + (size_t)(16 * j + n) * P);
+        for (int j = 0; j < NDT; ++j) f.v[j] = load_stream2(vt + 64 * j);
         if constexpr (USED) return ok ? used_cap(as_const(p.block_used)[row], slot0) : 0;
         return ok ? kTile : 0;
     };
@@ -471,8 +473,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
 
     // The staged new token of item c (segment s, position pos) into the pool, by the wave
     // that processes the item's tile holding it (or, for a token past the decoded tiles,
-    // the item's last decoded tile): the lanes that hold its K row and V column store them
-    // from LDS, with no wait.  Nothing in this launch reads these bytes back from the pool:
+    // the item's last decoded tile): the lanes that hold its K row store it, and every lane
+    // stores D / 64 elements of its V row, from LDS, with no wait.  Nothing in this launch reads these bytes back from the pool:
     // every reader of the tile patches the token in from LDS.  The bytes are those of
     // append_chunk<VSPEC_KV_F16>; a position past the table or an invalid block writes
     // nothing.
@@ -493,12 +495,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void decode_mfma_f16(DecodeParams 
                 kd[4 * i + g] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
             }
         }
-        if (g == ts / 4) {
-            uint16_t* vd = reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(p.v)) + bh * D * p.block_tokens + slot;
+        {
+            // the V row (stride 4 in its group of 4 tokens): every lane, D / 64 elements each, so
+            // that each store instruction covers whole 32-byte rows of the group
+            uint16_t* vd = reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(p.v)) + f16_v_index(bh, p.block_tokens, D, slot, 0);
 #pragma unroll
-            for (int j = 0; j < NDT; ++j) {
-                const int d = 16 * j + n;
-                vd[(size_t)d * p.block_tokens] = (uint16_t)(newtok[row][1][d / 2] >> (16 * (d & 1)));
+            for (int h = 0; h < D / 64; ++h) {
+                const int d = lane + 64 * h;
+                vd[4 * d] = (uint16_t)(newtok[row][1][d / 2] >> (16 * (d & 1)));
             }
         }
     };

@@ -118,6 +118,19 @@ __device__ __forceinline__ float row_dpp(float x) {
 }
 
 // ---------------------------------------------------------------------------
+// f16 pool layout (block_tokens a multiple of 16; bh = physical block * Hkv + head)
+//   K: token-major rows of D halves
+//   V: per (block, head), groups of 4 tokens: element (d, slot) at
+//      bh*D*P + (slot/4)*4*D + 4*d + slot%4.  A decode tile (16 tokens) is 4 KB in one
+//      piece; the MFMA operand of lane (g, n), 4 tokens of one d, is 8 contiguous bytes;
+//      and one token's row spans 1 KB (32 rows of 32 bytes), so a single token's
+//      append writes 4x fewer memory rows than in a d-major tile (128).
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ size_t f16_v_index(size_t bh, uint32_t P, uint32_t D, uint32_t slot, uint32_t d) {
+    return bh * D * P + (size_t)(slot >> 2) * (4u * D) + 4u * d + (slot & 3u);
+}
+
+// ---------------------------------------------------------------------------
 // int4 pool layout (block_tokens a multiple of 16; bh = physical block * Hkv + head)
 //   K codes : token-major rows of D/2 bytes, element e in nibble e%2 of byte e/2
 //   K scales: group-major, (group c, slot) at (bh*G + c)*P + slot

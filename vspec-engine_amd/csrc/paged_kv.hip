@@ -95,20 +95,16 @@ __device__ __forceinline__ void load_k16(const DecodeParams& p, size_t row, int 
     }
 }
 
-// V-side layout of the VALU decode kernel: D/8 lanes per token, lane chunk c holds
-// elements 8c..8c+7 (f16 V tiles are d-major, f32 token-major).
+// V-side layout of the VALU decode kernel (f32 pools: token-major rows): D/8 lanes per
+// token, lane chunk c holds elements 8c..8c+7.
 template <int DT, int D>
 __device__ __forceinline__ void load_v8(const DecodeParams& p, size_t row, int c, float* x) {
-    if constexpr (DT == VSPEC_KV_F16) {
-        const uint4 w = reinterpret_cast<const uint4*>(p.v + row * (size_t)(D * 2))[c];
-        unpack_f16x8(w, x);
-    } else {
-        const float4* src = reinterpret_cast<const float4*>(p.v + row * (size_t)(D * 4));
-        const float4 a = src[2 * c];
-        const float4 b = src[2 * c + 1];
-        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-    }
+    static_assert(DT == VSPEC_KV_F32, "the VALU decode kernel serves f32 pools");
+    const float4* src = reinterpret_cast<const float4*>(p.v + row * (size_t)(D * 4));
+    const float4 a = src[2 * c];
+    const float4 b = src[2 * c + 1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
 
 // Clip a row held by LPK lanes (16 elements each) to +-max(1e-6, alpha*std),
@@ -460,13 +456,12 @@ __global__ __launch_bounds__(256) void kv_gather(GatherParams p) {
         const uint8_t* src = which ? p.v : p.k;
         uint8_t* dst = which ? p.ov : p.ok;
         if (DT == VSPEC_KV_F16 && which) {
-            // d-major V tile: 8 elements of column `slot`, stride P
+            // V in 4-token groups: 8 elements of row `slot`, stride 4
             const uint16_t* vt = reinterpret_cast<const uint16_t*>(src) +
-                                 ((size_t)phys * p.hkv + h) * D * p.block_tokens + t % p.block_tokens;
-            const uint32_t d0 = 8 * c;
+                                 f16_v_index((size_t)phys * p.hkv + h, p.block_tokens, D, t % p.block_tokens, 8 * c);
             uint16_t e16[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) e16[i] = vt[(size_t)(d0 + i) * p.block_tokens];
+            for (int i = 0; i < 8; ++i) e16[i] = vt[4 * i];
             if (OUTF32) {
                 float4* d = reinterpret_cast<float4*>(dst + orow * (size_t)D * 4) + 2 * c;
                 d[0] = make_float4(half_bits_to_float(e16[0]), half_bits_to_float(e16[1]),
@@ -565,9 +560,9 @@ __global__ __launch_bounds__(256) void kv_gather_rows(GatherRowsParams p) {
             x[4] = bb.x; x[5] = bb.y; x[6] = bb.z; x[7] = bb.w;
         } else if constexpr (DT == VSPEC_KV_F16) {
             if (which) {
-                const uint16_t* vt = reinterpret_cast<const uint16_t*>(src) + tile * D * P + slot;
+                const uint16_t* vt = reinterpret_cast<const uint16_t*>(src) + f16_v_index(tile, P, D, slot, 8 * c);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = half_bits_to_float(vt[(size_t)(8 * c + e) * P]);
+                for (int e = 0; e < 8; ++e) x[e] = half_bits_to_float(vt[4 * e]);
             } else {
                 unpack_f16x8(reinterpret_cast<const uint4*>(src + row * D * 2)[c], x);
             }
@@ -675,8 +670,10 @@ int check_kv(const VspecPagedKV* kv, const char* who, bool decode = false) {
         set_err("%s: head_dim must be a multiple of %u", who, quantum);
         return 0;
     }
-    if (kv->dtype == VSPEC_KV_INT4 && kv->block_tokens % kTile != 0) {
-        set_err("%s: int4 pools need block_tokens a multiple of %d", who, kTile);
+    // int4 and f16 pools keep tiles of 16 tokens (f16 V: groups of 4 tokens, f16_v_index)
+    if (kv->dtype != VSPEC_KV_F32 && kv->block_tokens % kTile != 0) {
+        set_err("%s: %s pools need block_tokens a multiple of %d", who, kv->dtype == VSPEC_KV_INT4 ? "int4" : "f16",
+                kTile);
         return 0;
     }
     if (decode && kv->block_tokens % kTile != 0) {
