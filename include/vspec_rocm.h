@@ -10,23 +10,26 @@
  *   - no internal locking: calls that touch one pool are serialised by the caller
  *     (one stream per pool), as the reference's structs are unsynchronised.
  *
- * HBM layout (decision D6), element (block b, kv head h, slot s, dim d):
+ * HBM layout, element (block b, kv head h, slot s, dim d):
  *   K, and V of f32 pools  data[((b*H + h)*P + s)*D + d]          (token-major rows)
  *   V of f16 pools         data[(b*H + h)*D*P + (s/4)*4*D + 4*d + s%4]  (groups of 4 tokens,
  *                          d-major inside a group: the matrix-core operand of P.V needs 4
  *                          consecutive tokens of one d per lane, and one token's row then
  *                          spans 4*D halves instead of D*P)
- *   int4 pools (K and V)   codes byte ((b*H + h)*P + s)*(D/2) + d/2, nibble d&1 (even = low);
- *                          scale  ((b*H + h)*P + s)*(D/32) + d/32, fp16 bits
+ *   int4 K codes           byte ((b*H + h)*P + s)*(D/2) + d/2, nibble d&1 (even = low)
+ *   int4 K scales          ((b*H + h)*(D/32) + d/32)*P + s, fp16 bits (group-major)
+ *   int4 V codes           16-token tiles of 8*D bytes, lane chunk (g, n) at (16g + n)*(D/8)
+ *                          holds tokens 4g..4g+3 of d = 16j + n (two d-tiles per byte)
+ *   int4 V scales          ((b*H + h)*P + s)*(D/32) + d/32, fp16 bits
  * so one (block, head) tile of P tokens is contiguous (4 KB at P=16, D=128, f16).
  *
- * int4 codec (decision D1): per (token, kv head) groups of 32 elements;
+ * int4 codec: per (token, kv head) groups of 32 elements;
  *   rep   = 2nd-largest |x| of the group (kv_cache.c:32-59, percentile 99.5 at n=32)
  *   scale = rep > 0 ? rep/8 : 1, floored at 1e-6, rounded to fp16 (RNE, max 65504)
  *   code  = clip(rint(x / float(scale16)), -8, 7) with saturation (NaN -> -8)
  *   value = code * float(scale16)                 (exact in fp32)
  *
- * Attention numerics follow attention_ref.c:7-88 (decision D4): q and every k are
+ * Attention numerics follow attention_ref.c:7-88: q and every k are
  * clipped to +-max(1e-6, alpha*std) (three_bit_runtime_modules.c:175-203); with
  * VSPEC_NUMERICS_3BIT also to +-16 (:138-173), logits to +-24 (:205-250) and the
  * scale to [1e-4, 32] (:344-361).  GQA maps query head h to kv head h / (Hq/Hkv)
@@ -76,7 +79,7 @@ void vspec_rocm_kv_pool_destroy(VspecPagedKV* kv);
 /* ---- append: vspec_kv_paged_append (kv_paged_cache.c:243-310) for a batch ----
  * Writes n_new tokens per sequence at logical positions start_pos[b] .. +n_new-1
  * through the block table.  k_new / v_new: device [batch][n_new][H][D] in src_dtype
- * (VSPEC_KV_F32 or VSPEC_KV_F16).  An int4 pool quantises on write (D1).
+ * (VSPEC_KV_F32 or VSPEC_KV_F16).  An int4 pool quantises on write (the int4 codec above).
  * block_tables: device int32 [batch][max_blocks_per_seq]; start_pos: device int32 [batch]. */
 int vspec_rocm_kv_append(const VspecPagedKV* kv, uint32_t batch, const int32_t* block_tables,
                          uint32_t max_blocks_per_seq, const int32_t* start_pos, uint32_t n_new,

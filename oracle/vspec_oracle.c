@@ -313,7 +313,7 @@ void vo_int3_dequantize_head(const uint8_t* packed, const float* scales, size_t 
     }
 }
 
-/* int4 KV codec (D1), the b=4 generalisation of kv_cache.c:61-107 with fp16 scales
+/* int4 KV codec, the b=4 generalisation of kv_cache.c:61-107 with fp16 scales
  * and a saturating clip. */
 void vo_int4_quantize_head(const float* src, size_t head_dim, uint8_t* codes_out,
                            uint16_t* scales_out) {

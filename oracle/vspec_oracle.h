@@ -34,7 +34,7 @@ extern "C" {
 
 /* ---------------- fp16 ---------------- */
 float vo_half_to_float(uint16_t h);          /* q4_k.c:6-34 */
-uint16_t vo_float_to_half(float f);          /* IEEE RNE (format decision D2) */
+uint16_t vo_float_to_half(float f);          /* IEEE RNE */
 void vo_f16_to_f32(const uint16_t* src, float* dst, size_t n);
 void vo_f32_to_f16(const float* src, uint16_t* dst, size_t n);
 
@@ -60,7 +60,7 @@ void vo_int3_quantize_head(const float* src, size_t head_dim, size_t block_size,
                            uint8_t* packed_out, float* scales_out);
 void vo_int3_dequantize_head(const uint8_t* packed, const float* scales, size_t head_dim,
                              size_t block_size, float* out);
-/* int4 head codec (D1): groups of 32, fp16 scales.  head_dim % 32 == 0. */
+/* int4 head codec: groups of 32, fp16 scales.  head_dim % 32 == 0. */
 void vo_int4_quantize_head(const float* src, size_t head_dim, uint8_t* codes_out,
                            uint16_t* scales_out);
 void vo_int4_dequantize_head(const uint8_t* codes, const uint16_t* scales, size_t head_dim,
@@ -91,9 +91,10 @@ void vo_attention_ref_single_query(int mode, size_t dot_block, const float* quer
  * dtype: 0 = f32, 1 = f16, 2 = int4.
  * Element (block b, kv-head h, slot s, dim d):
  *   f32/f16 data index  ((b*H + h)*P + s)*D + d           (k_data / v_data)
- *   except f16 V        ((b*H + h)*D + d)*P + s           (d-major tiles)
- *   int4 code byte      ((b*H + h)*P + s)*(D/2) + d/2     (nibble d&1)
- *   int4 scale index    ((b*H + h)*P + s)*(D/32) + d/32   (k_scales / v_scales, fp16 bits)
+ *   except f16 V        (b*H + h)*D*P + (s/4)*4*D + 4*d + s%4  (groups of 4 tokens)
+ *   int4 K code byte    ((b*H + h)*P + s)*(D/2) + d/2     (nibble d&1)
+ *   int4 V scale index  ((b*H + h)*P + s)*(D/32) + d/32   (v_scales, fp16 bits)
+ *   int4 K scales and V codes: vo_int4_ks_index, vo_int4_v_byte (below)
  */
 typedef struct VoPagedKV {
     int dtype;
