@@ -65,7 +65,15 @@ def test_argument_validation_without_gpu():
     assert L.vspec_rocm_kv_append(C.byref(kv), 1, 0x1, 1, 0x1, 1, 0x1, 0x1, 1, None) == 0
     assert "multiple of 32" in vspec_rocm.last_error()
     kv.dtype = 1
-    # decode needs block_tokens % 16 == 0 and head_dim in {64, 128}; append and gather do not
+    # f16 pools keep 16-token tiles (V in groups of 4 tokens) for append and gather too
+    kv.head_dim, kv.block_tokens = 64, 24
+    assert L.vspec_rocm_kv_append(C.byref(kv), 1, 0x1, 1, 0x1, 1, 0x1, 0x1, 1, None) == 0
+    assert "f16 pools need block_tokens a multiple of 16" in vspec_rocm.last_error()
+    kv.dtype = 0  # f32 pools take any block size: the next error is the null-argument check
+    assert L.vspec_rocm_kv_append(C.byref(kv), 1, 0, 1, 0x1, 1, 0x1, 0x1, 0, None) == 0
+    assert "block_tokens" not in vspec_rocm.last_error()
+    kv.dtype = 1
+    # decode needs block_tokens % 16 == 0 and head_dim in {64, 128}
     dd = vspec_rocm.VspecPagedAttnDesc()
     dd.batch, dd.num_q_heads = 1, 4
     dd.kv = kv
