@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
     float(*comb)[GW][D + 2] = reinterpret_cast<float(*)[GW][D + 2]>(&stg[0][0]);
     __shared__ float qs[GW][D];
     __shared__ uint4 qb_lds[NQ][2][64];  // QK B operands (hi, lo) per lane
-    __shared__ float kbias_lds[16];       // per score column: the K bias' share (k_codes_to_f16)
+    __shared__ float kbias_lds[NQ][16];   // per score MFMA and column: the K bias' share (k_codes_to_f16)
     __shared__ int qexp_lds[4];           // per head: the q' operand shift (qnorm_shift)
     __shared__ float patch_val[kWaves][kTile][4];
     __shared__ int patch_flag[kWaves][kTile];
@@ -550,33 +550,35 @@ __global__ __launch_bounds__(256, VSPEC_I4_MIN_WG_PER_CU) void decode_mfma_i4(De
         // head h's operands carry q' * 2^e_h (qnorm_shift), taken back out of the scores by
         // qfac = 2^-e_h; the tile loop is instantiated twice, and only the one run for items
         // where some head has e != 0 (qnorm, wave-uniform) multiplies
-        if (wave == 0) {
+        // wave m builds the operands of score MFMA m (NQ <= kWaves)
+        if (wave < NQ) {
+            const int m = wave;
             const int hh = n & 3;
             const int hs = hh < GW ? hh : 0;
             const float qin = pow2i(qexp_lds[hs]);
             float odd = 0.f;  // this lane's B operands on the k-slots of odd elements
+            const int dw = g * NQ + m;
+            const bool on = (dw >> 2) == (n >> 2) && hh < GW;
+            h8_t hi8, lo8;
 #pragma unroll
-            for (int m = 0; m < NQ; ++m) {
-                const int dw = g * NQ + m;
-                const bool on = (dw >> 2) == (n >> 2) && hh < GW;
-                h8_t hi8, lo8;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int e = (j >> 1) + 4 * (j & 1);
-                    const float qv = qs[hs][8 * dw + e] * (on ? qin : 0.0f);
-                    const _Float16 hi = (_Float16)qv;
-                    hi8[j] = hi;
-                    lo8[j] = (_Float16)(qv - (float)hi);
-                    if (e & 1) odd += (float)hi8[j] + (float)lo8[j];
-                }
-                qb_lds[m][0][lane] = __builtin_bit_cast(uint4, hi8);
-                qb_lds[m][1][lane] = __builtin_bit_cast(uint4, lo8);
+            for (int j = 0; j < 8; ++j) {
+                const int e = (j >> 1) + 4 * (j & 1);
+                const float qv = qs[hs][8 * dw + e] * (on ? qin : 0.0f);
+                const _Float16 hi = (_Float16)qv;
+                hi8[j] = hi;
+                lo8[j] = (_Float16)(qv - (float)hi);
+                if (e & 1) odd += (float)hi8[j] + (float)lo8[j];
             }
+            qb_lds[m][0][lane] = __builtin_bit_cast(uint4, hi8);
+            qb_lds[m][1][lane] = __builtin_bit_cast(uint4, lo8);
             odd = add_rows(odd);
-            if (g == 0) kbias_lds[n] = 72.0f * odd;
+            if (g == 0) kbias_lds[m][n] = odd;
         }
         __syncthreads();
-        const float kbias = kbias_lds[n];
+        float kb = 0.f;
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) kb += kbias_lds[m][n];
+        const float kbias = 72.0f * kb;
         int qe_any = 0;
 #pragma unroll
         for (int h = 0; h < GW; ++h) qe_any |= qexp_lds[h];
