@@ -166,10 +166,12 @@ CacheSide cache_side(const VspecKVCache* c, bool value) {
 // ---------------------------------------------------------------------------
 // Persistent device mirror of a host VspecKVCache.
 //
-// The reference's caches grow append-only between attention calls (kv_cache.c:160-226:
-// rows go to current_tokens and the count increments), so a mirror keyed by the cache
-// keeps the rows already uploaded and each call uploads only the rows appended since the
-// last one.  head_dim 64 / 128: the rows are appended into a persistent f32 paged pool
+// The reference uploads the whole host cache on every attention call, and its caller owns
+// those rows; so by default every call uploads every row again into a mirror keyed by the
+// cache (device memory kept between calls).  A caller whose caches only grow between calls
+// (kv_cache.c:160-226: rows go to current_tokens and the count increments) can opt in to
+// uploading only the rows appended since the previous call (VSPEC_ROCM_MIRROR_APPEND_ONLY,
+// vspec_rocm_cache_mirror_append_only).  head_dim 64 / 128: the rows are appended into a persistent f32 paged pool
 // (identity block table, capacity max_tokens) and decoded by the paged kernels (Hq == Hkv);
 // other head sizes keep device [max_tokens][H][D] rows for the generic kernel.  Per call:
 // one upload of (q, the new rows or their int3 codes and scales) through pinned staging,
@@ -177,11 +179,12 @@ CacheSide cache_side(const VspecKVCache* c, bool value) {
 // output; after a mirror's first call no device memory is allocated or freed unless the
 // new rows outgrow the staging buffers.
 //
-// A mirror is reused when the cache pointer, its buffer pointers and geometry are the
-// same, current_tokens did not shrink, and fingerprints of the first token's rows and of
-// the last synced token's rows still match; anything else resyncs from token 0.  A caller
-// that rewrites rows in place keeps the contract by calling
-// vspec_rocm_release_cache_mirror (also to free the device memory with the cache).
+// In append-only mode the uploaded rows are kept when the cache pointer, its buffer
+// pointers and geometry are the same, current_tokens did not shrink, and fingerprints of
+// the first token's rows and of the last synced token's rows still match; anything else
+// resyncs from token 0.  A caller in that mode that rewrites rows in place keeps the
+// contract by calling vspec_rocm_release_cache_mirror (which also frees the device memory
+// with the cache).
 // ---------------------------------------------------------------------------
 struct Mirror {
     const VspecKVCache* cache = nullptr;
